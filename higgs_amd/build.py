@@ -1,0 +1,104 @@
+"""Build libhiggs_qmm.so for gfx950 with hipcc, in-tree.
+
+Every kernel source is compiled once per supported bit width with
+-DHQ_BITS=<b> (objects in higgs_amd/_build/), in parallel, then linked with
+the C ABI object into higgs_amd/libhiggs_qmm.so.
+
+    python -m higgs_amd.build            # full rebuild
+    python -m higgs_amd.build --incremental
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libhiggs_qmm.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+BITS = (2, 3, 4, 5, 6, 8)
+PER_BITS = ("hq_dequant.hip", "hq_qmv.hip", "hq_qmm.hip")
+ONCE = ("hq_capi.hip",)
+
+# -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 (see
+# DESIGN.md, hardware notes). Denormals are kept so fp16/fp32 dequantize
+# matches IEEE arithmetic bit for bit.
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-I", CSRC, "-I", INCLUDE,
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _headers_mtime() -> float:
+    hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hpp", ".h"))]
+    hs.append(os.path.join(INCLUDE, "higgs_qmm.h"))
+    return max(os.path.getmtime(h) for h in hs)
+
+
+def _jobs():
+    for src in PER_BITS:
+        for b in BITS:
+            obj = os.path.join(BUILD, f"{src[:-4]}_b{b}.o")
+            yield os.path.join(CSRC, src), obj, [f"-DHQ_BITS={b}"]
+    for src in ONCE:
+        yield os.path.join(CSRC, src), os.path.join(BUILD, f"{src[:-4]}.o"), []
+
+
+def _compile(src: str, obj: str, extra: list[str]) -> tuple[str, int, str]:
+    cmd = [HIPCC, *FLAGS, *extra, "-c", src, "-o", obj]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    return obj, p.returncode, (p.stdout + p.stderr)
+
+
+def build(incremental: bool = False, jobs: int | None = None, verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    hdr = _headers_mtime()
+    todo = []
+    objs = []
+    for src, obj, extra in _jobs():
+        objs.append(obj)
+        if incremental and os.path.exists(obj):
+            t = os.path.getmtime(obj)
+            if t >= os.path.getmtime(src) and t >= hdr:
+                continue
+        todo.append((src, obj, extra))
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    errors = []
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for obj, rc, out in ex.map(lambda j: _compile(*j), todo):
+            if rc != 0:
+                errors.append(f"--- {obj}\n{out}")
+            elif verbose and out.strip():
+                print(out, file=sys.stderr)
+    if errors:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(errors))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("link failed:\n" + p.stdout + p.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--incremental", action="store_true")
+    ap.add_argument("-j", "--jobs", type=int, default=None)
+    ap.add_argument("-v", "--verbose", action="store_true")
+    args = ap.parse_args()
+    print(build(args.incremental, args.jobs, args.verbose))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,113 @@
+// hq_dequant.hip -- dequantize and gathered-row dequantize (quantized
+// embedding lookup) for one bit width (HQ_BITS).
+//
+// out[r, k] = round(round(q * s) + b) in the scales' dtype: the product and
+// the sum each round separately (round-to-nearest-even), which is MLX's
+// op-by-op dequantize (multiply, then add) as reached from
+// crates/higgs-models/src/qwen3_next.rs:308-318. The kernel is HBM-bound:
+// each thread turns one 32-element pack (HQ_BITS words, 128-bit loads where
+// the width allows) into 32 outputs written with 128-bit stores.
+#include "hq_common.hpp"
+#include "hq_kernels.hpp"
+
+#ifndef HQ_BITS
+#error "compile with -DHQ_BITS=<2|3|4|5|6|8>"
+#endif
+
+namespace hq {
+
+template <int SDT>
+__device__ __forceinline__ float deq_round(uint32_t q, float s, float b) {
+#pragma clang fp contract(off)
+  float p = DT_<SDT>::round((float)q * s);
+  return DT_<SDT>::round(p + b);
+}
+
+template <int BITS, int SDT>
+__global__ __launch_bounds__(256) void dequant_kernel(st_t<SDT>* __restrict__ out,
+                                                       const uint32_t* __restrict__ w,
+                                                       const st_t<SDT>* __restrict__ s,
+                                                       const st_t<SDT>* __restrict__ b,
+                                                       const uint32_t* __restrict__ rows_idx,
+                                                       uint32_t total_packs, uint32_t ppr,
+                                                       int64_t src_rows, int gshift_packs) {
+  const int64_t K = (int64_t)ppr * 32;
+  const int64_t P = (int64_t)ppr * BITS;   // words per row
+  const int64_t G = (int64_t)ppr >> gshift_packs;  // groups per row
+  for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < total_packs; t += gridDim.x * 256u) {
+    const uint32_t r = t / ppr;
+    const uint32_t p = t - r * ppr;
+    const int64_t src = rows_idx ? (int64_t)rows_idx[r] : (int64_t)r;
+    st_t<SDT>* o = out + (int64_t)r * K + (int64_t)p * 32;
+    if constexpr (SDT == DT_F32) {
+      float v[32];
+      if (src >= src_rows) {
+#pragma unroll
+        for (int e = 0; e < 32; e++) v[e] = __uint_as_float(0x7fc00000u);
+      } else {
+        uint32_t wd[BITS];
+        load_pack<BITS>(w + src * P + (int64_t)p * BITS, wd);
+        const int64_t gi = src * G + (p >> gshift_packs);
+        const float sv = s[gi], bv = b[gi];
+#pragma unroll
+        for (int e = 0; e < 32; e++) v[e] = deq_round<SDT>(pack_elem<BITS>(wd, e), sv, bv);
+      }
+      float4* o4 = reinterpret_cast<float4*>(o);
+#pragma unroll
+      for (int i = 0; i < 8; i++) o4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    } else {
+      uint32_t h[16];
+      if (src >= src_rows) {
+        const uint32_t nan2 = SDT == DT_BF16 ? 0x7fc07fc0u : 0x7e007e00u;
+#pragma unroll
+        for (int i = 0; i < 16; i++) h[i] = nan2;
+      } else {
+        uint32_t wd[BITS];
+        load_pack<BITS>(w + src * P + (int64_t)p * BITS, wd);
+        const int64_t gi = src * G + (p >> gshift_packs);
+        const float sv = DT_<SDT>::load(s, gi), bv = DT_<SDT>::load(b, gi);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          uint32_t lo = DT_<SDT>::from_f32(deq_round<SDT>(pack_elem<BITS>(wd, 2 * i), sv, bv));
+          uint32_t hi = DT_<SDT>::from_f32(deq_round<SDT>(pack_elem<BITS>(wd, 2 * i + 1), sv, bv));
+          h[i] = lo | (hi << 16);
+        }
+      }
+      u32x4* o4 = reinterpret_cast<u32x4*>(o);
+#pragma unroll
+      for (int i = 0; i < 4; i++) o4[i] = u32x4{h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]};
+    }
+  }
+}
+
+#define HQ_CAT_(a, b) a##b
+#define HQ_CAT(a, b) HQ_CAT_(a, b)
+
+hipError_t HQ_CAT(launch_dequant_b, HQ_BITS)(const DeqArgs& a) {
+  const uint32_t ppr = (uint32_t)(a.K / 32);
+  const uint64_t total = (uint64_t)a.n_rows * ppr;
+  const int gsp = __builtin_ctz((unsigned)(a.group_size / 32));
+  uint32_t blocks = (uint32_t)((total + 255) / 256);
+  if (blocks > 65536u * 8u) blocks = 65536u * 8u;
+  if (blocks == 0) return hipSuccess;
+  switch (a.sdt) {
+    case DT_F32:
+      dequant_kernel<HQ_BITS, DT_F32><<<blocks, 256, 0, a.stream>>>(
+          (float*)a.out, a.w, (const float*)a.s, (const float*)a.b, a.rows_idx, (uint32_t)total, ppr,
+          a.src_rows, gsp);
+      break;
+    case DT_F16:
+      dequant_kernel<HQ_BITS, DT_F16><<<blocks, 256, 0, a.stream>>>(
+          (uint16_t*)a.out, a.w, (const uint16_t*)a.s, (const uint16_t*)a.b, a.rows_idx, (uint32_t)total,
+          ppr, a.src_rows, gsp);
+      break;
+    default:
+      dequant_kernel<HQ_BITS, DT_BF16><<<blocks, 256, 0, a.stream>>>(
+          (uint16_t*)a.out, a.w, (const uint16_t*)a.s, (const uint16_t*)a.b, a.rows_idx, (uint32_t)total,
+          ppr, a.src_rows, gsp);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace hq

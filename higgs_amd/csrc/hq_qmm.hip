@@ -1,0 +1,240 @@
+// hq_qmm.hip -- quantized GEMM for prefill (M > 8), one bit width (HQ_BITS).
+//
+// y = x . deq(W)^T (mlx-rs ops::quantized_matmul, transpose=true, as called
+// from crates/higgs-models/src/qwen3_next.rs:218-227 and the Llama
+// MaybeQuantized layers, crates/higgs-models/src/transformer.rs:257-259).
+//
+// Each 256-thread block computes a BM x BN tile of y. Per K step the block
+// stages the x tile in LDS (converted to the compute type) and dequantizes the
+// W tile straight into LDS as s*q+b rounded to the compute type, so the MFMA
+// operands never leave the chip. Compute type: bf16 (16x16x32 bf16 MFMA) for
+// bf16 x and scales, fp16 likewise, fp32 (16x16x4 fp32 MFMA) otherwise, all
+// with fp32 accumulation. Gathered batches (gather_qmm with M > 8) use
+// blockIdx.z.
+#include "hq_common.hpp"
+#include "hq_kernels.hpp"
+
+#ifndef HQ_BITS
+#error "compile with -DHQ_BITS=<2|3|4|5|6|8>"
+#endif
+
+namespace hq {
+
+struct QKernM {
+  void* y;
+  const void* x;
+  const uint32_t* w;
+  const void* s;
+  const void* b;
+  const uint32_t* lhs;
+  const uint32_t* rhs;
+  int64_t batch, x_rep, x_batch, w_batch;
+  int M, N, K;
+  int gshift;
+};
+
+template <int CT> struct Mma;
+template <> struct Mma<DT_BF16> {
+  static constexpr int KW = 32, E = 8, BK = 64, PAD = 8;
+  using lds_t = uint16_t;
+  using frag = bf16x8;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t cvt(float v) { return f32_to_bf16_bits(v); }
+};
+template <> struct Mma<DT_F16> {
+  static constexpr int KW = 32, E = 8, BK = 64, PAD = 8;
+  using lds_t = uint16_t;
+  using frag = f16x8;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t cvt(float v) { return f32_to_f16_bits(v); }
+};
+template <> struct Mma<DT_F32> {
+  static constexpr int KW = 4, E = 1, BK = 32, PAD = 4;
+  using lds_t = float;
+  using frag = float;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int BM = 128, BN = 128;
+
+template <int BITS, int XDT, int SDT>
+__global__ __launch_bounds__(256) void qmm_t_kernel(QKernM a) {
+  constexpr int CT = (XDT == SDT && XDT != DT_F32) ? XDT : DT_F32;
+  constexpr int ODT = result_dtype(XDT, SDT);
+  using T = Mma<CT>;
+  using L = typename T::lds_t;
+  using XS = st_t<XDT>;
+  using SS = st_t<SDT>;
+  using OS = st_t<ODT>;
+  constexpr int BK = T::BK;
+  constexpr int LD = BK + T::PAD;  // LDS row stride in elements
+  constexpr int A_CHUNKS = BM * BK / 8 / 256;    // 8-element chunks per thread
+  constexpr int B_PACKS = BN * BK / 32;          // 32-element packs per stage
+  __shared__ __attribute__((aligned(16))) L As[BM * LD];
+  __shared__ __attribute__((aligned(16))) L Bs[BN * LD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int M = a.M, N = a.N, K = a.K;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int64_t P = (int64_t)(K >> 5) * BITS;
+  const int64_t G = K >> a.gshift;
+  const int gsp = a.gshift - 5;
+
+  for (int64_t bi = blockIdx.z; bi < a.batch; bi += gridDim.z) {
+    const int64_t xi = a.lhs ? (int64_t)a.lhs[bi] : bi / a.x_rep;
+    const int64_t wi = a.rhs ? (int64_t)a.rhs[bi] : 0;
+    OS* yb = (OS*)a.y + bi * (int64_t)M * N;
+    const bool bad = xi >= a.x_batch || wi >= a.w_batch;
+    const XS* xb = (const XS*)a.x + (bad ? 0 : xi) * (int64_t)M * K;
+    const uint32_t* wb = a.w + (bad ? 0 : wi) * (int64_t)N * P;
+    const SS* sb = (const SS*)a.s + (bad ? 0 : wi) * (int64_t)N * G;
+    const SS* bb = (const SS*)a.b + (bad ? 0 : wi) * (int64_t)N * G;
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int k0 = 0; k0 < K && !bad; k0 += BK) {
+      // ---- stage x tile (BM x BK) ----
+#pragma unroll
+      for (int c = 0; c < A_CHUNKS; c++) {
+        const int chunk = tid + c * 256;
+        const int row = chunk / (BK / 8), kc = chunk % (BK / 8);
+        const int gm = m0 + row, gk = k0 + kc * 8;
+        L* dst = &As[row * LD + kc * 8];
+        if (gm < M && gk < K) {
+          const XS* src = xb + (int64_t)gm * K + gk;
+          if constexpr (CT == XDT && CT != DT_F32) {
+            *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+          } else {
+            float v[8];
+            load8_f32<XDT>(src, v);
+            if constexpr (CT == DT_F32) {
+#pragma unroll
+              for (int e = 0; e < 8; e++) dst[e] = v[e];
+            } else {
+              u32x4 h;
+#pragma unroll
+              for (int e = 0; e < 4; e++) h[e] = T::cvt(v[2 * e]) | (T::cvt(v[2 * e + 1]) << 16);
+              *reinterpret_cast<u32x4*>(dst) = h;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; e++) dst[e] = (L)0;
+        }
+      }
+      // ---- dequantize W tile (BN x BK) ----
+      for (int pk = tid; pk < B_PACKS; pk += 256) {
+        const int row = pk / (BK / 32), pc = pk % (BK / 32);
+        const int gn = n0 + row, gk = k0 + pc * 32;
+        L* dst = &Bs[row * LD + pc * 32];
+        if (gn < N && gk < K) {
+          uint32_t wd[BITS];
+          load_pack<BITS>(wb + (int64_t)gn * P + (int64_t)(gk >> 5) * BITS, wd);
+          const int64_t gi = (int64_t)gn * G + ((gk >> 5) >> gsp);
+          const float sv = DT_<SDT>::load(sb, gi), bv = DT_<SDT>::load(bb, gi);
+          if constexpr (CT == DT_F32) {
+#pragma unroll
+            for (int e = 0; e < 32; e++) dst[e] = fmaf(sv, (float)pack_elem<BITS>(wd, e), bv);
+          } else {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+              u32x4 h;
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                const int i0 = q4 * 8 + 2 * e;
+                h[e] = T::cvt(fmaf(sv, (float)pack_elem<BITS>(wd, i0), bv)) |
+                       (T::cvt(fmaf(sv, (float)pack_elem<BITS>(wd, i0 + 1), bv)) << 16);
+              }
+              *reinterpret_cast<u32x4*>(dst + q4 * 8) = h;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 32; e++) dst[e] = (L)0;
+        }
+      }
+      __syncthreads();
+      // ---- MFMA over the stage ----
+#pragma unroll
+      for (int ks = 0; ks < BK / T::KW; ks++) {
+        typename T::frag fa[4], fb[4];
+        const int kofs = ks * T::KW + (lane >> 4) * T::E;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const L* pa = &As[(wm * 64 + i * 16 + (lane & 15)) * LD + kofs];
+          const L* pb = &Bs[(wn * 64 + i * 16 + (lane & 15)) * LD + kofs];
+          if constexpr (CT == DT_F32) {
+            fa[i] = *pa;
+            fb[i] = *pb;
+          } else {
+            fa[i] = __builtin_bit_cast(typename T::frag, *reinterpret_cast<const u32x4*>(pa));
+            fb[i] = __builtin_bit_cast(typename T::frag, *reinterpret_cast<const u32x4*>(pb));
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) acc[i][j] = T::mma(fa[i], fb[j], acc[i][j]);
+      }
+      __syncthreads();
+    }
+    // ---- epilogue ----
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          const int gm = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + v;
+          const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
+          if (gm < M && gn < N) {
+            const float o = bad ? __uint_as_float(0x7fc00000u) : acc[i][j][v];
+            yb[(int64_t)gm * N + gn] = DT_<ODT>::from_f32(o);
+          }
+        }
+  }
+}
+
+template <int XDT, int SDT>
+static void run_qmm_t(const QArgs& a) {
+  QKernM k;
+  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
+  k.lhs = a.lhs; k.rhs = a.rhs;
+  k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
+  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
+  k.gshift = __builtin_ctz((unsigned)a.group_size);
+  dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM),
+            (unsigned)(a.batch < 65535 ? a.batch : 65535));
+  qmm_t_kernel<HQ_BITS, XDT, SDT><<<grid, 256, 0, a.stream>>>(k);
+}
+
+#define HQ_CAT_(a, b) a##b
+#define HQ_CAT(a, b) HQ_CAT_(a, b)
+
+hipError_t HQ_CAT(launch_qmm_t_b, HQ_BITS)(const QArgs& a) {
+  switch (a.xdt * 3 + a.sdt) {
+    case DT_F32 * 3 + DT_F32: run_qmm_t<DT_F32, DT_F32>(a); break;
+    case DT_F32 * 3 + DT_F16: run_qmm_t<DT_F32, DT_F16>(a); break;
+    case DT_F32 * 3 + DT_BF16: run_qmm_t<DT_F32, DT_BF16>(a); break;
+    case DT_F16 * 3 + DT_F32: run_qmm_t<DT_F16, DT_F32>(a); break;
+    case DT_F16 * 3 + DT_F16: run_qmm_t<DT_F16, DT_F16>(a); break;
+    case DT_F16 * 3 + DT_BF16: run_qmm_t<DT_F16, DT_BF16>(a); break;
+    case DT_BF16 * 3 + DT_F32: run_qmm_t<DT_BF16, DT_F32>(a); break;
+    case DT_BF16 * 3 + DT_F16: run_qmm_t<DT_BF16, DT_F16>(a); break;
+    default: run_qmm_t<DT_BF16, DT_BF16>(a); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace hq

@@ -1,0 +1,299 @@
+"""Host-side facade of the quantized-linear path over the C ABI.
+
+Mirrors the mlx-rs operator interface that higgs' model layers call, with the
+same argument names, meanings and validation messages:
+
+* ``quantized_matmul(x, w, scales, biases, transpose, group_size, bits)`` --
+  mlx-rs ``ops::quantized_matmul`` (crates/higgs-models/src/qwen3_next.rs:
+  218-227; every mlx-rs ``QuantizedLinear``, transformer.rs:148-157).
+* ``gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices, transpose,
+  group_size, bits, sorted_indices)`` -- ``mlx_gather_qmm`` as wrapped by
+  higgs' ``gather_qmm`` (qwen3_next.rs:509-578).
+* ``dequantize(w, scales, biases, group_size, bits)`` -- mlx-rs
+  ``ops::dequantize`` (qwen3_next.rs:314).
+
+Tensors are torch tensors on the GPU: torch provides device memory and the
+current HIP stream, and the arithmetic runs in libhiggs_qmm.so. Packed weights
+are ``torch.uint32`` or ``torch.int32`` (same bits). There is no CPU fallback:
+CPU tensors are rejected.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import HiggsQmmError
+
+_DT = {torch.float32: _lib.DTYPE_FLOAT32, torch.float16: _lib.DTYPE_FLOAT16,
+       torch.bfloat16: _lib.DTYPE_BFLOAT16}
+_TORCH_DT = {v: k for k, v in _DT.items()}
+_WORD_DTYPES = (torch.int32, getattr(torch, "uint32", torch.int32))
+_INDEX_DTYPES = (torch.int32, getattr(torch, "uint32", torch.int32), torch.int64)
+
+SUPPORTED_BITS = (2, 3, 4, 5, 6, 8)
+SUPPORTED_GROUP_SIZES = (32, 64, 128)
+
+
+def _err(msg: str, status: int = _lib.HQ_ERR_INVALID_ARGUMENT) -> HiggsQmmError:
+    return HiggsQmmError(status, msg)
+
+
+def _shape(t: torch.Tensor) -> str:
+    return "(" + ",".join(str(d) for d in t.shape) + ")"
+
+
+def _dt_name(t: torch.Tensor) -> str:
+    return str(t.dtype).replace("torch.", "")
+
+
+def _check_params(tag: str, group_size: int, bits: int) -> None:
+    if bits not in SUPPORTED_BITS:
+        raise _err(f"[{tag}] The requested number of bits {bits} is not supported. "
+                   "The supported bits are 2, 3, 4, 5, 6 and 8.")
+    if group_size not in SUPPORTED_GROUP_SIZES:
+        raise _err(f"[{tag}] The requested group size {group_size} is not supported. "
+                   "The supported group sizes are 32, 64, and 128.")
+
+
+def _check_device(tag: str, *ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise _err(f"[{tag}] All arrays must live on the GPU (got a tensor on {t.device}).")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise _err(f"[{tag}] All arrays must be on the same device.")
+    return dev
+
+
+def _words(tag: str, w: torch.Tensor) -> torch.Tensor:
+    if w.dtype not in _WORD_DTYPES:
+        raise _err(f"[{tag}] The weight matrix should be uint32 but received {_dt_name(w)}")
+    return w.contiguous()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def result_dtype(x_dtype: torch.dtype, s_dtype: torch.dtype) -> torch.dtype:
+    """MLX promotion of the activation and scale dtypes (mixed -> float32)."""
+    return x_dtype if x_dtype == s_dtype else torch.float32
+
+
+def _extract_dims(tag, x, w, scales, biases, transpose, group_size, bits):
+    """MLX's extract_quantized_matmul_dims: returns (w_inner, w_outer)."""
+    w = _words(tag, w)
+    if scales.shape != biases.shape:
+        raise _err(f"[{tag}] Scales and biases should have the same shape. Received scales "
+                   f"with shape {_shape(scales)} and biases with {_shape(biases)}.")
+    if w.dim() < 2 or scales.dim() != w.dim() or tuple(w.shape[:-2]) != tuple(scales.shape[:-2]):
+        raise _err(f"[{tag}] Weight, scales and biases should have the same batch shape. "
+                   f"Received weight with shape {_shape(w)}, scales with {_shape(scales)} "
+                   f"and biases with {_shape(biases)}.")
+    if w.shape[-1] * 32 // bits != scales.shape[-1] * group_size or \
+            w.shape[-1] * 32 % bits or w.shape[-2] != scales.shape[-2]:
+        raise _err(f"[{tag}] The shapes of the weight and scales are incompatible based on bits "
+                   f"and group_size. w.shape() == {_shape(w)} and scales.shape() == "
+                   f"{_shape(scales)} with group_size={group_size} and bits={bits}")
+    w_inner = w.shape[-1] * 32 // bits if transpose else w.shape[-2]
+    w_outer = w.shape[-2] if transpose else w.shape[-1] * 32 // bits
+    if x.shape[-1] != w_inner:
+        raise _err(f"[{tag}] Last dimension of first input with shape (..., {x.shape[-1]}) does "
+                   f"not match the expanded quantized matrix ({w_inner}, {w_outer}) computed "
+                   f"from shape {_shape(w)} with group_size={group_size}, bits={bits} and "
+                   f"transpose={str(bool(transpose)).lower()}")
+    for t, name in ((x, "x"), (scales, "scales"), (biases, "biases")):
+        if t.dtype not in _DT:
+            raise _err(f"[{tag}] Only real floating types are supported but x.dtype() == "
+                       f"{_dt_name(x)}, scales.dtype() == {_dt_name(scales)} and "
+                       f"biases.dtype() == {_dt_name(biases)}")
+    if scales.dtype != biases.dtype:
+        raise _err(f"[{tag}] scales and biases must share a dtype (got {_dt_name(scales)} and "
+                   f"{_dt_name(biases)}).")
+    return w, w_inner, w_outer
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, transpose: bool = True, group_size: int = 64,
+                     bits: int = 4) -> torch.Tensor:
+    """y = x @ deq(w).T (transpose) or x @ deq(w); x is [..., K].
+
+    A 2-D ``w`` is one product with all of x's leading dims flattened into M.
+    A batched ``w`` ([..., N, P]) broadcasts its batch dims against x's, as MLX
+    does, and runs through the gather kernel with default indices.
+    """
+    tag = "quantized_matmul"
+    _check_params(tag, group_size, bits)
+    if x.dim() < 1:
+        raise _err(f"[{tag}] x must have at least one dimension.")
+    w, w_inner, w_outer = _extract_dims(tag, x, w, scales, biases, transpose, group_size, bits)
+    dev = _check_device(tag, x, w, scales, biases)
+    out_dtype = result_dtype(x.dtype, scales.dtype)
+    if w.dim() > 2:
+        if x.dim() < 2:
+            x = x.unsqueeze(0)
+        return gather_qmm(x, w, scales, biases, None, None, transpose, group_size, bits, False)
+    x = x.contiguous()
+    scales = scales.contiguous()
+    biases = biases.contiguous()
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    y = torch.empty((*x.shape[:-1], w_outer), dtype=out_dtype, device=dev)
+    _lib.check(_lib.lib().hq_quantized_matmul(
+        _ptr(y), _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), M, w_outer, K,
+        int(bool(transpose)), group_size, bits, _DT[x.dtype], _DT[scales.dtype], _stream(dev)))
+    return y
+
+
+def _prefix_broadcast(x_batch_shape: Sequence[int], out_shape: Sequence[int]) -> bool:
+    """True if x's batch dims, right-aligned to out_shape, equal a prefix of out_shape
+    followed only by 1s -- then x batch element = flat_out_index // (batch/x_batch)."""
+    nd = len(out_shape)
+    if len(x_batch_shape) > nd:
+        return False
+    xs = [1] * (nd - len(x_batch_shape)) + list(x_batch_shape)
+    j = nd
+    while j > 0 and xs[j - 1] == 1:
+        j -= 1
+    return all(xs[i] == out_shape[i] for i in range(j))
+
+
+def _as_u32_indices(tag: str, idx: torch.Tensor, name: str) -> torch.Tensor:
+    if idx.dtype not in _INDEX_DTYPES:
+        raise _err(f"[{tag}] {name} must be an integer array (got {_dt_name(idx)}).")
+    if idx.dtype == torch.int64:
+        idx = idx.to(torch.int32)
+    return idx.contiguous()
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               lhs_indices: Optional[torch.Tensor] = None,
+               rhs_indices: Optional[torch.Tensor] = None, transpose: bool = True,
+               group_size: int = 64, bits: int = 4,
+               sorted_indices: bool = False) -> torch.Tensor:
+    """MLX gather_qmm: out[b] = x[lhs[b]] @ deq(w[rhs[b]]).T for the broadcast of
+    lhs_indices and rhs_indices; x is [..., M, K], w is [..., N, P].
+
+    Output shape: broadcast(lhs, rhs).shape + [M, N]. Missing indices default to
+    an arange over the batch dims of x (lhs) or w (rhs), as MLX does.
+    """
+    tag = "gather_qmm"
+    _check_params(tag, group_size, bits)
+    if x.dim() < 2 or w.dim() < 2:
+        raise _err(f"[{tag}] x and w must have at least two dimensions.")
+    w, w_inner, w_outer = _extract_dims(tag, x, w, scales, biases, transpose, group_size, bits)
+    dev = _check_device(tag, x, w, scales, biases, lhs_indices, rhs_indices)
+    x_batch_shape = tuple(x.shape[:-2])
+    w_batch_shape = tuple(w.shape[:-2])
+    x_batch = math.prod(x_batch_shape)
+    w_batch = math.prod(w_batch_shape)
+    M, K = x.shape[-2], x.shape[-1]
+    N = w_outer
+    if rhs_indices is None:
+        rhs = torch.arange(w_batch, dtype=torch.int32, device=dev).reshape(w_batch_shape)
+    else:
+        rhs = _as_u32_indices(tag, rhs_indices, "rhs_indices")
+    lhs = None if lhs_indices is None else _as_u32_indices(tag, lhs_indices, "lhs_indices")
+    lhs_shape = x_batch_shape if lhs is None else tuple(lhs.shape)
+    try:
+        out_batch = tuple(torch.broadcast_shapes(lhs_shape, tuple(rhs.shape)))
+    except RuntimeError:
+        raise _err(f"[{tag}] Cannot broadcast lhs indices with shape {lhs_shape} and rhs "
+                   f"indices with shape {tuple(rhs.shape)}.") from None
+    batch = math.prod(out_batch)
+    out_dtype = result_dtype(x.dtype, scales.dtype)
+    y = torch.empty((*out_batch, M, N), dtype=out_dtype, device=dev)
+    if y.numel() == 0:
+        return y
+    rhs_flat = rhs.expand(out_batch).contiguous().reshape(-1)
+    if lhs is None and _prefix_broadcast(x_batch_shape, out_batch):
+        lhs_flat = None
+    else:
+        if lhs is None:
+            lhs = torch.arange(x_batch, dtype=torch.int32, device=dev).reshape(x_batch_shape)
+        lhs_flat = lhs.expand(out_batch).contiguous().reshape(-1)
+    x = x.contiguous()
+    scales = scales.contiguous()
+    biases = biases.contiguous()
+    _lib.check(_lib.lib().hq_gather_qmm(
+        _ptr(y), _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(lhs_flat), _ptr(rhs_flat),
+        batch, max(x_batch, 1), max(w_batch, 1), M, N, K, int(bool(transpose)), group_size, bits,
+        int(bool(sorted_indices)), _DT[x.dtype], _DT[scales.dtype], _stream(dev)))
+    return y
+
+
+def _check_dequant(tag, w, scales, biases, group_size, bits):
+    _check_params(tag, group_size, bits)
+    if w.dim() < 2 or scales.dim() < 2 or biases.dim() < 2:
+        raise _err(f"[{tag}] The matrix to be quantized must have at least 2 dimension but it "
+                   f"has only {w.dim()}.")
+    if tuple(w.shape[:-1]) != tuple(scales.shape[:-1]) or \
+            tuple(w.shape[:-1]) != tuple(biases.shape[:-1]):
+        raise _err(f"[{tag}] Shape of scales and biases does not match the matrix")
+    if w.dtype not in _WORD_DTYPES:
+        raise _err(f"[{tag}] The matrix should be given as a uint32")
+    if w.shape[-1] * 32 // bits != scales.shape[-1] * group_size or w.shape[-1] * 32 % bits:
+        raise _err(f"[{tag}] Shape of scales and biases does not match the matrix given the "
+                   f"quantization parameters. Provided matrix of shape {_shape(w)} and "
+                   f"scales/biases of shape {_shape(scales)} with group_size={group_size} and "
+                   f"bits={bits}.")
+    if scales.dtype not in _DT or biases.dtype != scales.dtype:
+        raise _err(f"[{tag}] scales and biases must be float32, float16 or bfloat16 and share a "
+                   "dtype.")
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """deq(w) = scales * q + biases in the scales' dtype; out is w.shape[:-1] + [K]."""
+    tag = "dequantize"
+    _check_dequant(tag, w, scales, biases, group_size, bits)
+    dev = _check_device(tag, w, scales, biases)
+    w = w.contiguous()
+    scales = scales.contiguous()
+    biases = biases.contiguous()
+    K = w.shape[-1] * 32 // bits
+    rows = w.numel() // w.shape[-1] if w.shape[-1] else 0
+    out = torch.empty((*w.shape[:-1], K), dtype=scales.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    _lib.check(_lib.lib().hq_dequantize(_ptr(out), _ptr(w), _ptr(scales), _ptr(biases), rows, K,
+                                        group_size, bits, _DT[scales.dtype], _stream(dev)))
+    return out
+
+
+def embedding(indices: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+              biases: torch.Tensor, group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """Quantized embedding lookup, dequantize(w[idx], scales[idx], biases[idx]).
+
+    higgs' QEmbedding::forward (crates/higgs-models/src/qwen3_next.rs:308-318):
+    flatten indices, take rows, dequantize, reshape to indices.shape + [K]. Only
+    the selected rows are read.
+    """
+    tag = "embedding"
+    _check_dequant(tag, w, scales, biases, group_size, bits)
+    if w.dim() != 2:
+        raise _err(f"[{tag}] The embedding table must be 2-D (got {_shape(w)}).")
+    dev = _check_device(tag, w, scales, biases, indices)
+    flat = _as_u32_indices(tag, indices, "indices").reshape(-1)
+    K = w.shape[-1] * 32 // bits
+    out = torch.empty((*indices.shape, K), dtype=scales.dtype, device=dev)
+    if out.numel() == 0:
+        return out
+    w = w.contiguous()
+    scales = scales.contiguous()
+    biases = biases.contiguous()
+    _lib.check(_lib.lib().hq_embedding_dequantize(
+        _ptr(out), _ptr(w), _ptr(scales), _ptr(biases), _ptr(flat), flat.numel(), w.shape[0], K,
+        group_size, bits, _DT[scales.dtype], _stream(dev)))
+    return out

@@ -1,0 +1,157 @@
+/*
+ * higgs_qmm.h -- C ABI of the MI355X (gfx950) MLX-format affine
+ * group-quantized linear path: quantized_matmul (qmv for decode, qmm for
+ * prefill), gather_qmm (MoE experts) and dequantize.
+ *
+ * Conventions shared by every entry point
+ *  - All data pointers are device pointers (HBM), caller-owned. Nothing in
+ *    this library allocates device memory for these calls.
+ *  - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
+ *    on it and the call returns without synchronising.
+ *  - Quantized matrices use MLX's layout: a logical [rows, cols] matrix of
+ *    `bits`-bit unsigned integers is stored as uint32 [rows, cols*bits/32];
+ *    element i of a row sits at bit i*bits of the row's little-endian
+ *    bitstream, least significant bits first (3-, 5- and 6-bit values
+ *    straddle word boundaries). scales and biases are [rows, cols/group_size]
+ *    and dequantize as  w = scale * q + bias.
+ *  - bits in {2, 3, 4, 5, 6, 8}; group_size in {32, 64, 128}.
+ *  - x_dtype / s_dtype are hq_dtype codes for the activations and for the
+ *    scales+biases. The output dtype follows MLX promotion:
+ *    hq_result_dtype(x_dtype, s_dtype) (equal -> same, mixed -> float32).
+ *  - Return value: HQ_OK (0) or an hq_status error; the message of the last
+ *    error on the calling thread is returned by hq_last_error().
+ *  - Calls on one stream are ordered; the library keeps no per-call state,
+ *    so concurrent calls from several threads on different streams are safe.
+ */
+#ifndef HIGGS_QMM_H
+#define HIGGS_QMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HQ_ABI_VERSION 1
+
+typedef enum hq_status {
+  HQ_OK = 0,
+  HQ_ERR_INVALID_ARGUMENT = 1, /* shape / dtype / bits / group_size rejected */
+  HQ_ERR_UNSUPPORTED = 2,      /* valid for MLX but not implemented here */
+  HQ_ERR_HIP = 3               /* a HIP runtime call or kernel launch failed */
+} hq_status;
+
+typedef enum hq_dtype {
+  HQ_DTYPE_FLOAT32 = 0,
+  HQ_DTYPE_FLOAT16 = 1,
+  HQ_DTYPE_BFLOAT16 = 2
+} hq_dtype;
+
+/* Library version string, e.g. "higgs_qmm 0.1.0 (gfx950)". */
+const char* hq_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* hq_last_error(void);
+
+/* Output dtype of quantized_matmul / gather_qmm for these input dtypes, or
+ * -1 if either code is not an hq_dtype. */
+int hq_result_dtype(int x_dtype, int s_dtype);
+
+/*
+ * y = x . deq(W)^T  (transpose != 0) or  y = x . deq(W)  (transpose == 0).
+ *
+ * Replaces mlx-rs ops::quantized_matmul(x, w, scales, biases, transpose,
+ * group_size, bits) as called by higgs' QLinear / quantized_forward
+ * (crates/higgs-models/src/qwen3_next.rs:218-227, 255-264), QEmbedding::
+ * as_linear (qwen3_next.rs:320-333), the fused dense FFN
+ * (qwen3_next.rs:2539-2585) and every MaybeQuantized nn::Linear
+ * (crates/higgs-models/src/transformer.rs:148-157, 257-259, 355-356, 843-847).
+ *
+ *   x: [M, K] of x_dtype (all leading batch dims of MLX's x flattened into M)
+ *   transpose != 0: w [N, K*bits/32], scales/biases [N, K/group_size]
+ *   transpose == 0: w [K, N*bits/32], scales/biases [K, N/group_size]
+ *   y: [M, N] of hq_result_dtype(x_dtype, s_dtype)
+ *
+ * M == 0 or N == 0 is a valid empty call. K must be a positive multiple of
+ * group_size when transpose != 0 (N likewise when transpose == 0).
+ */
+int hq_quantized_matmul(void* y, const void* x, const uint32_t* w,
+                        const void* scales, const void* biases, int64_t M,
+                        int64_t N, int64_t K, int transpose, int group_size,
+                        int bits, int x_dtype, int s_dtype, void* stream);
+
+/*
+ * Batched quantized matmul with expert gather.
+ *
+ * Replaces mlx_sys::mlx_gather_qmm(res, x, w, scales, biases, lhs_indices,
+ * rhs_indices, transpose, group_size, bits, "affine", sorted_indices, stream)
+ * as wrapped by higgs' gather_qmm (crates/higgs-models/src/qwen3_next.rs:
+ * 509-578) and called by SwitchMlpWeights::forward_gather /
+ * forward_gather_global_sort (qwen3_next.rs:1660-1720, 1731-1809).
+ *
+ *   x: [x_batch, M, K]; w: [w_batch, N, K*bits/32] (transpose != 0) or
+ *   [w_batch, K, N*bits/32] (transpose == 0); scales/biases: [w_batch, rows,
+ *   cols/group_size]; lhs_indices, rhs_indices: uint32 [batch] (already
+ *   broadcast against each other); y: [batch, M, N].
+ *
+ *   For i in [0, batch):
+ *     xi = lhs_indices ? lhs_indices[i] : i / (batch / x_batch)
+ *     wi = rhs_indices[i]
+ *     y[i] = x[xi] . deq(W[wi])^T   (or . deq(W[wi]) when transpose == 0)
+ *
+ * lhs_indices == NULL is MLX's null-lhs sentinel for the broadcast higgs
+ * uses: x's batch dims are a prefix of the output batch dims, each x batch
+ * element repeated batch/x_batch times (batch % x_batch must be 0). Other
+ * broadcasts pass explicit lhs_indices.
+ * sorted_indices != 0 promises rhs_indices is non-decreasing (the global
+ * expert sort); it selects the grouped kernel that reads each expert's
+ * weights once per run of equal indices. Results do not depend on it.
+ * Indices out of range (xi >= x_batch or wi >= w_batch) never cause an
+ * out-of-bounds read: their output rows are filled with NaN.
+ */
+int hq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
+                  const void* biases, const uint32_t* lhs_indices,
+                  const uint32_t* rhs_indices, int64_t batch, int64_t x_batch,
+                  int64_t w_batch, int64_t M, int64_t N, int64_t K,
+                  int transpose, int group_size, int bits, int sorted_indices,
+                  int x_dtype, int s_dtype, void* stream);
+
+/*
+ * out = scales * q + biases, in the scales' dtype (s_dtype).
+ *
+ * Replaces mlx-rs ops::dequantize(w, scales, biases, group_size, bits) as
+ * called by higgs' QEmbedding::forward (crates/higgs-models/src/
+ * qwen3_next.rs:308-318).
+ *
+ *   w: [rows, K*bits/32]; scales/biases: [rows, K/group_size]; out: [rows, K].
+ *
+ * Rounding: for 16-bit scales each element is round(round(q*s) + b) -- the
+ * product and the sum each rounded to s_dtype (round-to-nearest-even), as
+ * MLX's op-by-op dequantize computes it; for float32 scales the product and
+ * the sum each round to float32 (no fused multiply-add).
+ */
+int hq_dequantize(void* out, const uint32_t* w, const void* scales,
+                  const void* biases, int64_t rows, int64_t K, int group_size,
+                  int bits, int s_dtype, void* stream);
+
+/*
+ * Row gather then dequantize: out[i] = deq(W[indices[i]]), i in [0, n).
+ *
+ * Replaces the take_axis(w/scales/biases) + ops::dequantize sequence of
+ * higgs' QEmbedding::forward (crates/higgs-models/src/qwen3_next.rs:308-318),
+ * fused so that only the selected rows are read.
+ *
+ *   w: [rows, K*bits/32]; scales/biases: [rows, K/group_size];
+ *   indices: uint32 [n]; out: [n, K] of s_dtype. Rows whose index is
+ *   >= rows are filled with NaN.
+ */
+int hq_embedding_dequantize(void* out, const uint32_t* w, const void* scales,
+                            const void* biases, const uint32_t* indices,
+                            int64_t n, int64_t rows, int64_t K, int group_size,
+                            int bits, int s_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIGGS_QMM_H */

@@ -1,0 +1,156 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects bad arguments (with MLX-style messages) before any
+HIP call is made. Mirrors the error path higgs relies on
+(crates/higgs-models/src/qwen3_next.rs:552-576: status != 0 plus a message)."""
+import os
+import re
+import threading
+
+import pytest
+import torch
+
+from higgs_amd import _lib, ops
+from higgs_amd._lib import HiggsQmmError
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "higgs_qmm.h")
+FAKE = 0x7F0000000000  # never dereferenced: validation fails before any launch
+
+
+def header_symbols():
+    txt = open(HEADER).read()
+    return set(re.findall(r"^(?:const\s+)?(?:char\s*\*|int|void)\s*\*?\s*(hq_\w+)\s*\(", txt, re.M))
+
+
+def test_exports_every_header_symbol():
+    syms = header_symbols()
+    assert {"hq_quantized_matmul", "hq_gather_qmm", "hq_dequantize", "hq_last_error",
+            "hq_version", "hq_result_dtype", "hq_embedding_dequantize"} <= syms
+    L = _lib.lib()
+    for s in syms:
+        assert hasattr(L, s), s
+    assert set(_lib.SIGNATURES) == syms
+
+
+def test_version_and_result_dtype():
+    assert "gfx950" in _lib.version()
+    L = _lib.lib()
+    F32, F16, BF16 = 0, 1, 2
+    table = {(F32, F32): F32, (F16, F16): F16, (BF16, BF16): BF16, (BF16, F16): F32,
+             (F16, BF16): F32, (F32, BF16): F32, (BF16, F32): F32}
+    for (a, b), r in table.items():
+        assert L.hq_result_dtype(a, b) == r
+    assert L.hq_result_dtype(3, 0) == -1
+
+
+def qmm(**kw):
+    a = dict(y=FAKE, x=FAKE, w=FAKE, s=FAKE, b=FAKE, M=1, N=64, K=128, transpose=1, g=64,
+             bits=4, xdt=2, sdt=2)
+    a.update(kw)
+    return _lib.lib().hq_quantized_matmul(a["y"], a["x"], a["w"], a["s"], a["b"], a["M"],
+                                          a["N"], a["K"], a["transpose"], a["g"], a["bits"],
+                                          a["xdt"], a["sdt"], None)
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(bits=7), "bits 7 is not supported"),
+    (dict(bits=1), "bits 1 is not supported"),
+    (dict(g=16), "group size 16 is not supported"),
+    (dict(K=96), "divisible by the group size"),
+    (dict(transpose=0, N=100, g=64), "divisible by the group size"),
+    (dict(xdt=7), "floating"),
+    (dict(sdt=-1), "floating"),
+    (dict(M=-1), "Invalid sizes"),
+    (dict(K=0), "Invalid sizes"),
+    (dict(y=0), "NULL"),
+    (dict(w=0), "NULL"),
+    (dict(x=FAKE + 8), "16-byte aligned"),
+])
+def test_quantized_matmul_rejects(kw, needle):
+    rc = qmm(**kw)
+    assert rc == _lib.HQ_ERR_INVALID_ARGUMENT
+    assert needle in _lib.last_error()
+
+
+def test_empty_calls_succeed_without_gpu():
+    assert qmm(M=0) == 0
+    assert qmm(N=0) == 0
+    L = _lib.lib()
+    assert L.hq_gather_qmm(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 0, 1, 4, 1, 64, 128, 1, 64,
+                           4, 1, 2, 2, None) == 0
+    assert L.hq_dequantize(FAKE, FAKE, FAKE, FAKE, 0, 128, 64, 4, 2, None) == 0
+    assert L.hq_embedding_dequantize(FAKE, FAKE, FAKE, FAKE, None, 0, 10, 128, 64, 4, 2,
+                                     None) == 0
+
+
+def test_gather_rejects():
+    L = _lib.lib()
+
+    def call(lhs=None, rhs=FAKE, batch=8, xb=8, wb=4, bits=4, g=64):
+        return L.hq_gather_qmm(FAKE, FAKE, FAKE, FAKE, FAKE, lhs, rhs, batch, xb, wb, 1, 64, 128,
+                               1, g, bits, 1, 2, 2, None)
+
+    assert call(rhs=None) == 1 and "rhs_indices" in _lib.last_error()
+    assert call(batch=6, xb=4) == 1 and "multiple of x's batch" in _lib.last_error()
+    assert call(wb=0) == 1 and "Invalid sizes" in _lib.last_error()
+    assert call(bits=9) == 1
+
+
+def test_dequantize_rejects():
+    L = _lib.lib()
+    assert L.hq_dequantize(FAKE, FAKE, FAKE, FAKE, 4, 100, 64, 4, 2, None) == 1
+    assert "multiple of the group" in _lib.last_error()
+    assert L.hq_dequantize(FAKE + 4, FAKE, FAKE, FAKE, 4, 128, 64, 4, 2, None) == 1
+    assert L.hq_embedding_dequantize(FAKE, FAKE, FAKE, FAKE, None, 3, 10, 128, 64, 4, 2,
+                                     None) == 1
+    assert "indices" in _lib.last_error()
+
+
+def test_last_error_is_thread_local():
+    assert qmm(bits=7) == 1
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(_lib.last_error()))
+    t.start()
+    t.join()
+    assert seen == [""]
+    assert "bits 7" in _lib.last_error()
+
+
+# --- host facade validation (mirrors MLX's messages; CPU tensors suffice) ----
+
+def _q(N=64, K=128, bits=4, g=64, lead=()):
+    w = torch.zeros((*lead, N, K * bits // 32), dtype=torch.int32)
+    s = torch.zeros((*lead, N, K // g), dtype=torch.bfloat16)
+    return w, s, s.clone()
+
+
+def test_facade_shape_errors():
+    w, s, b = _q()
+    x = torch.zeros(1, 128, dtype=torch.bfloat16)
+    with pytest.raises(HiggsQmmError, match="Scales and biases should have the same shape"):
+        ops.quantized_matmul(x, w, s, b[:, :1])
+    with pytest.raises(HiggsQmmError, match="incompatible based on bits and group_size"):
+        ops.quantized_matmul(x, w, s, b, group_size=32)
+    with pytest.raises(HiggsQmmError, match="does not match the expanded quantized matrix"):
+        ops.quantized_matmul(torch.zeros(1, 64, dtype=torch.bfloat16), w, s, b)
+    with pytest.raises(HiggsQmmError, match="should be uint32"):
+        ops.quantized_matmul(x, w.float(), s, b)
+    with pytest.raises(HiggsQmmError, match="bits 7 is not supported"):
+        ops.quantized_matmul(x, w, s, b, bits=7)
+    with pytest.raises(HiggsQmmError, match="Only real floating types"):
+        ops.quantized_matmul(x.to(torch.int32), w, s, b)
+    with pytest.raises(HiggsQmmError, match="must live on the GPU"):
+        ops.quantized_matmul(x, w, s, b)
+    with pytest.raises(HiggsQmmError, match="Shape of scales and biases does not match"):
+        ops.dequantize(w, s[:, :1], b[:, :1])
+    with pytest.raises(HiggsQmmError, match="at least two dimensions"):
+        ops.gather_qmm(x[0], w, s, b, rhs_indices=torch.zeros(1, dtype=torch.int32))
+
+
+def test_prefix_broadcast_rule():
+    pb = ops._prefix_broadcast
+    assert pb((2, 3, 1), (2, 3, 8))      # forward_gather: x [B,L,1] vs idx [B,L,k]
+    assert pb((4096,), (4096,))          # global sort: one x row per index
+    assert pb((1,), (7,)) and pb((), (7,))
+    assert not pb((3,), (2, 3))          # x broadcast along a leading dim
+    assert not pb((1, 3), (2, 3))

@@ -1,0 +1,288 @@
+"""Parity of the HIP path (through the C ABI, via the torch facade) with the
+CPU oracle on identical seeded inputs.
+
+Bars: dequantize bit-exact (two-rounding convention, include/higgs_qmm.h);
+quantized_matmul / gather_qmm max relative error (max|y-r| / max|r| against the
+oracle's fp64 result) <= 1e-2 for bf16/fp16 output and <= 1e-3 for fp32 output.
+Shapes: small ones the oracle finishes in seconds, plus the BASELINE configs at
+full size, compared on sampled weight rows (each sampled row is an exact
+sub-problem, so the check is size independent).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import (TOL, idx_dev, quant, rel_err, to_dev, to_host_bits, to_host_f64,
+                     words_dev, x_of)
+from higgs_amd import gen, ops
+
+pytestmark = pytest.mark.gpu
+
+BITS = (2, 3, 4, 5, 6, 8)
+GROUPS = (32, 64, 128)
+
+
+def _qmm_check(dev, M, N, K, bits, g, xdt, sdt, seed=0, transpose=True, lead_x=None):
+    rows, cols = (N, K) if transpose else (K, N)
+    w, s, b = quant(seed, rows, cols, bits, g, sdt)
+    x = x_of(seed + 7, (M, K), xdt)
+    y = ops.quantized_matmul(to_dev(x, xdt, dev), words_dev(w, dev), to_dev(s, sdt, dev),
+                             to_dev(b, sdt, dev), transpose, g, bits)
+    odt = O.result_dtype(xdt, sdt)
+    assert y.dtype == {O.F32: torch.float32, O.F16: torch.float16, O.BF16: torch.bfloat16}[odt]
+    assert tuple(y.shape) == (M, N)
+    ref = O.qmm_f64(x, xdt, w, s, b, sdt, g, bits, transpose=transpose)
+    err = rel_err(to_host_f64(y), ref)
+    assert err <= TOL[odt], (M, N, K, bits, g, xdt, sdt, err)
+    return err
+
+
+# --- dequantize ---------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("g", GROUPS)
+@pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32])
+def test_dequantize_bit_exact(dev, bits, g, dt):
+    w, s, b = quant(bits * 10 + g, 37, 384, bits, g, dt)
+    out = ops.dequantize(words_dev(w, dev), to_dev(s, dt, dev), to_dev(b, dt, dev), g, bits)
+    ref = O.dequantize(w, s, b, g, bits, dt)
+    np.testing.assert_array_equal(to_host_bits(out), ref)
+
+
+def test_dequantize_bit_exact_c0_shape(dev):
+    # [8192, 2048] 4-bit g64, bf16 scales
+    w, s, b = quant(1, 8192, 2048, 4, 64, O.BF16)
+    out = ops.dequantize(words_dev(w, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev), 64, 4)
+    np.testing.assert_array_equal(to_host_bits(out), O.dequantize(w, s, b, 64, 4, O.BF16))
+
+
+def test_dequantize_batched_leading_dims(dev):
+    w, s, b = quant(3, 6, 256, 3, 32, O.BF16, lead=(2,))
+    out = ops.dequantize(words_dev(w, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev), 32, 3)
+    assert tuple(out.shape) == (2, 6, 256)
+    ref = O.dequantize(w.reshape(12, -1), s.reshape(12, -1), b.reshape(12, -1), 32, 3, O.BF16)
+    np.testing.assert_array_equal(to_host_bits(out).reshape(12, -1), ref)
+
+
+def test_embedding_gather_then_dequantize_equivalence(dev):
+    # qwen3_next.rs:12374-12412: take-then-dequantize == dequantize-then-take
+    w, s, b = quant(5, 256, 128, 4, 64, O.BF16)
+    W, S, B = words_dev(w, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev)
+    idx = np.array([[0, 5, 42], [255, 5, 7]], np.uint32)
+    emb = ops.embedding(idx_dev(idx, dev), W, S, B, 64, 4)
+    assert tuple(emb.shape) == (2, 3, 128)
+    full = ops.dequantize(W, S, B, 64, 4)
+    np.testing.assert_array_equal(to_host_bits(emb), to_host_bits(full[idx_dev(idx, dev).long()]))
+    bad = ops.embedding(idx_dev(np.array([256, 1], np.uint32), dev), W, S, B, 64, 4)
+    assert torch.isnan(bad[0]).all() and not torch.isnan(bad[1]).any()
+
+
+# --- quantized_matmul: decode GEMV --------------------------------------------
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("g", GROUPS)
+def test_qmv_bf16_all_bits_groups(dev, bits, g):
+    for M in (1, 3, 8):
+        _qmm_check(dev, M, 200, 512, bits, g, O.BF16, O.BF16, seed=bits + g)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8])
+@pytest.mark.parametrize("xdt,sdt", [(O.F32, O.F32), (O.F16, O.F16), (O.BF16, O.F16),
+                                     (O.F32, O.BF16), (O.F16, O.BF16), (O.BF16, O.F32)])
+def test_qmv_dtypes(dev, M, xdt, sdt):
+    _qmm_check(dev, M, 96, 384, 4, 64, xdt, sdt, seed=M)
+
+
+# --- quantized_matmul: prefill GEMM -------------------------------------------
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("g", [32, 128])
+def test_qmm_bf16_all_bits(dev, bits, g):
+    _qmm_check(dev, 70, 160, 384, bits, g, O.BF16, O.BF16, seed=bits)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 64, 64), (128, 128, 128), (200, 300, 96), (513, 257, 320)])
+@pytest.mark.parametrize("xdt,sdt", [(O.BF16, O.BF16), (O.F16, O.F16), (O.F32, O.F32),
+                                     (O.BF16, O.F16)])
+def test_qmm_shapes_dtypes(dev, M, N, K, xdt, sdt):
+    _qmm_check(dev, M, N, K, 4, 32, xdt, sdt, seed=M + N)
+
+
+def test_qmm_leading_dims_flatten(dev):
+    w, s, b = quant(2, 64, 128, 4, 64, O.BF16)
+    x = x_of(3, (2, 5, 128), O.BF16)
+    y = ops.quantized_matmul(to_dev(x, O.BF16, dev), words_dev(w, dev), to_dev(s, O.BF16, dev),
+                             to_dev(b, O.BF16, dev), True, 64, 4)
+    assert tuple(y.shape) == (2, 5, 64)
+    ref = O.qmm_f64(x.reshape(10, 128), O.BF16, w, s, b, O.BF16, 64, 4)
+    assert rel_err(to_host_f64(y).reshape(10, 64), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("M", [1, 4, 33])
+@pytest.mark.parametrize("bits", [3, 4, 8])
+def test_no_transpose(dev, M, bits):
+    _qmm_check(dev, M, 128, 100, bits, 64, O.BF16, O.BF16, seed=M, transpose=False)
+
+
+def test_empty_and_minimal(dev):
+    w, s, b = quant(4, 16, 32, 4, 32, O.BF16)
+    W, S, B = words_dev(w, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev)
+    y = ops.quantized_matmul(torch.zeros(0, 32, dtype=torch.bfloat16, device=dev), W, S, B, True,
+                             32, 4)
+    assert tuple(y.shape) == (0, 16)
+    _qmm_check(dev, 1, 1, 32, 4, 32, O.BF16, O.BF16)
+    _qmm_check(dev, 17, 1, 32, 4, 32, O.BF16, O.BF16)
+
+
+def test_fused_gate_up_equals_separate(dev):
+    # qwen3_next.rs:13132-13169: one qmv over concat(gate, up) == two qmvs
+    wg, sg, bg = quant(11, 96, 64, 4, 32, O.F16)
+    wu, su, bu = quant(12, 96, 64, 4, 32, O.F16)
+    x = to_dev(x_of(13, (1, 64), O.F16), O.F16, dev)
+    d = lambda a, dt=O.F16: to_dev(a, dt, dev)
+    fused = ops.quantized_matmul(x, words_dev(np.concatenate([wg, wu]), dev),
+                                 d(np.concatenate([sg, su])), d(np.concatenate([bg, bu])), True,
+                                 32, 4)
+    g_ = ops.quantized_matmul(x, words_dev(wg, dev), d(sg), d(bg), True, 32, 4)
+    u_ = ops.quantized_matmul(x, words_dev(wu, dev), d(su), d(bu), True, 32, 4)
+    assert torch.equal(fused, torch.cat([g_, u_], dim=-1))
+
+
+def test_qmv_equals_qmm_rows(dev):
+    # qwen3_next.rs:12929-13006 (custom qgemv vs quantized_matmul): the GEMV path
+    # (M <= 8) and the GEMM path (M > 8) agree row by row within tolerance.
+    w, s, b = quant(14, 256, 1024, 4, 64, O.BF16)
+    W, S, B = words_dev(w, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev)
+    x = to_dev(x_of(15, (16, 1024), O.BF16), O.BF16, dev)
+    big = ops.quantized_matmul(x, W, S, B, True, 64, 4).float()
+    for r in (0, 7, 15):
+        one = ops.quantized_matmul(x[r:r + 1], W, S, B, True, 64, 4).float()
+        assert (one - big[r:r + 1]).abs().max() <= 1e-2 * big.abs().max()
+
+
+# --- gather_qmm ---------------------------------------------------------------
+
+def _experts(seed, E, N, K, bits, g, dt=O.BF16):
+    return quant(seed, N, K, bits, g, dt, lead=(E,))
+
+
+def test_gather_matches_per_expert(dev):
+    # qwen3_next.rs:4344-4398
+    w, s, b = _experts(20, 4, 64, 64, 4, 64)
+    W, S, B = words_dev(w, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev)
+    x = to_dev(x_of(21, (1, 64), O.BF16), O.BF16, dev)
+    old = ops.quantized_matmul(x, W[2], S[2], B[2], True, 64, 4)
+    new = ops.gather_qmm(x.unsqueeze(-2), W, S, B, None, idx_dev(np.array([[2]]), dev), True, 64,
+                         4, False)
+    assert tuple(new.shape) == (1, 1, 1, 64)
+    assert torch.equal(old.reshape(-1), new.reshape(-1))
+
+
+def test_gather_shapes_like_reference(dev):
+    # qwen3_next.rs:4310-4341, 4626-4708: output shape contracts
+    w, s, b = _experts(22, 8, 64, 64, 4, 64)
+    W, S, B = words_dev(w, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev)
+    x = to_dev(x_of(23, (1, 9, 1, 1, 64), O.BF16), O.BF16, dev)
+    idx = np.array([0, 1, 2, 3, 4, 5, 6, 7, 0, 1, 2, 3, 4, 5, 6, 7, 0, 7], np.uint32).reshape(1, 9, 2)
+    y = ops.gather_qmm(x, W, S, B, None, idx_dev(idx, dev), True, 64, 4, False)
+    assert tuple(y.shape) == (1, 9, 2, 1, 64)
+    ref = O.gather_qmm_f64(x_of(23, (9, 1, 64), O.BF16), O.BF16, w, s, b, O.BF16, None,
+                           idx.reshape(-1), 1, 64, 64, 64, 4)
+    assert rel_err(to_host_f64(y).reshape(18, 1, 64), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("M", [1, 3, 12])
+@pytest.mark.parametrize("bits", [3, 4, 8])
+def test_gather_vs_oracle(dev, M, bits):
+    E, N, K, g = 6, 96, 256, 64
+    w, s, b = _experts(30 + M, E, N, K, bits, g)
+    x = x_of(31, (5, M, K), O.BF16)
+    rng = np.random.default_rng(M)
+    lhs = rng.integers(0, 5, 11).astype(np.uint32)
+    rhs = rng.integers(0, E, 11).astype(np.uint32)
+    y = ops.gather_qmm(to_dev(x, O.BF16, dev), words_dev(w, dev), to_dev(s, O.BF16, dev),
+                       to_dev(b, O.BF16, dev), idx_dev(lhs, dev), idx_dev(rhs, dev), True, g, bits)
+    ref = O.gather_qmm_f64(x, O.BF16, w, s, b, O.BF16, lhs, rhs, M, N, K, g, bits)
+    assert rel_err(to_host_f64(y), ref) <= 1e-2
+
+
+def test_gather_out_of_range_gives_nan(dev):
+    w, s, b = _experts(40, 3, 64, 128, 4, 64)
+    x = x_of(41, (2, 1, 128), O.BF16)
+    y = ops.gather_qmm(to_dev(x, O.BF16, dev), words_dev(w, dev), to_dev(s, O.BF16, dev),
+                       to_dev(b, O.BF16, dev), idx_dev(np.array([0, 1, 7]), dev),
+                       idx_dev(np.array([3, 1, 0]), dev), True, 64, 4)
+    assert torch.isnan(y[0]).all() and torch.isnan(y[2]).all()
+    assert not torch.isnan(y[1]).any()
+
+
+def test_sorted_equals_unsorted_and_global_sort_roundtrip(dev):
+    # qwen3_next.rs:4431-4530 (global sort == baseline), 1731-1809 (sort/unsort)
+    E, D, I, L, k = 8, 64, 64, 16, 3
+    wg, sg, bg = _experts(50, E, I, D, 4, 64)
+    x = x_of(51, (1, L, D), O.BF16)
+    idx = (np.arange(L * k) % E).astype(np.uint32).reshape(1, L, k)
+    Wd, Sd, Bd = words_dev(wg, dev), to_dev(sg, O.BF16, dev), to_dev(bg, O.BF16, dev)
+    xd = to_dev(x, O.BF16, dev)
+    base = ops.gather_qmm(xd.reshape(1, L, 1, 1, D), Wd, Sd, Bd, None, idx_dev(idx, dev), True,
+                          64, 4, False).reshape(L * k, I)
+    order, inv, srt, tok = O.gather_sort(idx, k)
+    xs = xd.reshape(L, 1, D)[torch.from_numpy(tok.astype(np.int64)).to(dev)]
+    ys = ops.gather_qmm(xs, Wd, Sd, Bd, None, idx_dev(srt, dev), True, 64, 4, True).reshape(-1, I)
+    unsorted = ys[torch.from_numpy(inv.astype(np.int64)).to(dev)]
+    assert torch.equal(unsorted, base)
+
+
+@pytest.mark.parametrize("xdt,sdt", [(O.F32, O.F32), (O.F16, O.F16), (O.BF16, O.F16)])
+def test_gather_dtypes(dev, xdt, sdt):
+    w, s, b = _experts(60, 4, 64, 128, 4, 32, sdt)
+    x = x_of(61, (6, 2, 128), xdt)
+    rhs = np.array([3, 0, 0, 1, 2, 3], np.uint32)
+    y = ops.gather_qmm(to_dev(x, xdt, dev), words_dev(w, dev), to_dev(s, sdt, dev),
+                       to_dev(b, sdt, dev), None, idx_dev(rhs, dev), True, 32, 4)
+    ref = O.gather_qmm_f64(x, xdt, w, s, b, sdt, None, rhs, 2, 64, 128, 32, 4)
+    assert rel_err(to_host_f64(y), ref) <= TOL[O.result_dtype(xdt, sdt)]
+
+
+# --- BASELINE configs at full size (sampled rows) -----------------------------
+
+def _sampled_rows_check(dev, M, N, K, bits, g, seed, n_rows=384, bias_noise=1e-3):
+    W, S, B = gen.torch_quantized(seed, N, K, bits, g, dev, bias_noise=bias_noise)
+    X = gen.torch_x(seed + 1, (M, K), dev)
+    Y = ops.quantized_matmul(X, W, S, B, True, g, bits)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([[0, N - 1], rng.integers(0, N, n_rows)]))
+    rt = torch.from_numpy(rows).to(dev)
+    w = W[rt].cpu().numpy().view(np.uint32)
+    s = S[rt].cpu().view(torch.int16).numpy().view(np.uint16)
+    b = B[rt].cpu().view(torch.int16).numpy().view(np.uint16)
+    x = X.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = O.qmm_f64(x, O.BF16, w, s, b, O.BF16, g, bits)
+    err = rel_err(to_host_f64(Y[:, rt]), ref)
+    assert err <= 1e-2, (M, N, K, bits, g, err)
+
+
+@pytest.mark.parametrize("B", [1, 4, 8])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336),
+                                 (128256, 4096)])
+def test_c1_llama3_8b_decode_shapes(dev, B, N, K):
+    _sampled_rows_check(dev, B, N, K, 4, 64, seed=N + K + B)
+
+
+def test_c0_llama32_1b_up(dev):
+    _sampled_rows_check(dev, 1, 8192, 2048, 4, 64, seed=0)
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+def test_c2_prefill_2048(dev, N, K):
+    _sampled_rows_check(dev, 2048, N, K, 4, 64, seed=N, n_rows=64)
+
+
+@pytest.mark.parametrize("bits,g", [(2, 64), (3, 64), (8, 64), (4, 32), (4, 128)])
+@pytest.mark.parametrize("M", [1, 512])
+def test_c3_qwen3_bit_group_sweep(dev, bits, g, M):
+    for N, K in ((6144, 2048), (2048, 6144)):
+        _sampled_rows_check(dev, M, N, K, bits, g, seed=bits * 100 + g + M, n_rows=128,
+                            bias_noise=0.0)

@@ -1,0 +1,294 @@
+"""Pins the CPU oracle (oracle/hq_oracle.c) before it is trusted as the checker.
+
+The reference ships no golden vectors for this path (its hot-path tests are
+relational, MLX-vs-MLX on unkeyed random inputs), so each oracle function is
+pinned by something independent of its own code: a library routine (torch's
+bf16/fp16 rounding and elementwise ops, numpy float64 matmul and stable
+argsort), a closed form or special case, an independent construction (Python
+big integers for the bitstream), or the reference's relational invariants
+(crates/higgs-models/src/qwen3_next.rs:4344-4398, 4431-4530, 12374-12412).
+Each check is chosen so that a plausible slip -- nibble order reversed, a
+dropped bias, a wrong group index, transposed operands, an unstable sort --
+fails it.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from higgs_amd import gen
+
+BITS = (2, 3, 4, 5, 6, 8)
+GROUPS = (32, 64, 128)
+TORCH16 = {O.BF16: torch.bfloat16, O.F16: torch.float16}
+
+
+def _special_floats():
+    v = [0.0, -0.0, 1.0, -1.0, 65504.0, 65519.0, 65520.0, 1e-8, 6e-8, 5.96e-8, 2.98e-8,
+         6.1035156e-05, 6.09e-05, 3.0e38, -3.0e38, np.inf, -np.inf, 1.0 + 2 ** -8,
+         1.0 + 2 ** -9, 1.0 + 3 * 2 ** -9, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 2 ** -126,
+         2 ** -149, 2 ** -25, 2 ** -24, 1.5 * 2 ** -25, 3 * 2 ** -26]
+    rng = np.random.default_rng(1)
+    r = np.concatenate([rng.standard_normal(20000) * s for s in (1e-6, 1e-3, 1, 1e3, 1e5)])
+    # exact halfway points between neighbouring bf16 / fp16 values
+    base = rng.standard_normal(4000).astype(np.float32)
+    bh = (base.view(np.uint32) & 0xFFFF0000) | 0x8000
+    fh = (base.view(np.uint32) & 0xFFFFE000) | 0x1000
+    return np.concatenate([np.array(v, np.float32), r.astype(np.float32),
+                           bh.view(np.float32), fh.view(np.float32)])
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+def test_rounding_matches_torch(orc, dt):
+    v = _special_floats()
+    got = orc.from_f32(v, dt)
+    ref = torch.from_numpy(v).to(TORCH16[dt]).view(torch.int16).numpy().view(np.uint16)
+    finite = np.isfinite(v)
+    np.testing.assert_array_equal(got[finite], ref[finite])
+    # widening is exact: round trip through the oracle's own to_f32
+    back = orc.to_f32(got, dt)
+    np.testing.assert_array_equal(back[finite],
+                                  torch.from_numpy(ref.view(np.int16)).view(TORCH16[dt])
+                                  .float().numpy()[finite])
+
+
+def test_nan_is_canonical(orc):
+    v = np.array([np.nan, -np.nan], np.float32)
+    assert list(orc.from_f32(v, O.BF16)) == [0x7FC0, 0x7FC0]
+    assert all(x & 0x7FFF == 0x7E00 for x in orc.from_f32(v, O.F16))
+
+
+# --- packing ----------------------------------------------------------------
+
+def test_unpack_nibble_order_kat(orc):
+    # qwen3_next.rs:978-986: (packed >> 4*i) & 0xF is element 8*j + i of word j
+    w = np.array([[0x76543210, 0xFEDCBA98]], np.uint32)
+    assert orc.unpack(w, 4).tolist() == [list(range(16))]
+    assert orc.unpack(np.array([[0x04030201]], np.uint32), 8).tolist() == [[1, 2, 3, 4]]
+    w2 = np.array([[0b11100100 | (0b00011011 << 8)] + [0] * 1], np.uint32)
+    assert orc.unpack(w2, 2)[0, :8].tolist() == [0, 1, 2, 3, 3, 2, 1, 0]
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_pack_matches_bigint_bitstream(orc, bits):
+    rng = np.random.default_rng(bits)
+    rows, cols = 5, 128
+    q = rng.integers(0, 2 ** bits, size=(rows, cols), dtype=np.uint32)
+    w = orc.pack(q, bits)
+    for r in range(rows):
+        acc = 0
+        for i, v in enumerate(q[r].tolist()):
+            acc |= v << (bits * i)
+        raw = acc.to_bytes(cols * bits // 8, "little")
+        np.testing.assert_array_equal(w[r], np.frombuffer(raw, "<u4"))
+    np.testing.assert_array_equal(orc.unpack(w, bits), q)
+    # the product-side packer (higgs_amd.gen) agrees with the oracle
+    np.testing.assert_array_equal(gen.pack_bits(q, bits), w)
+
+
+def test_three_bit_straddles_words(orc):
+    q = np.zeros((1, 32), np.uint32)
+    q[0, 10] = 0b101  # bits 30,31 of word 0 and bit 0 of word 1
+    w = orc.pack(q, 3)
+    assert w[0, 0] == (0b01 << 30) and w[0, 1] == 0b1
+
+
+# --- dequantize -------------------------------------------------------------
+
+def _quant(seed, rows, K, bits, g, dt):
+    w, s, b = gen.np_quantized(seed, rows, K, bits, g)
+    if dt == O.F32:
+        s = gen.bf16_bits_to_f32(s) * np.float32(1.37)
+        b = gen.bf16_bits_to_f32(b) * np.float32(0.71)
+    elif dt == O.F16:
+        s = torch.from_numpy(gen.bf16_bits_to_f32(s)).half().view(torch.int16).numpy().view(np.uint16)
+        b = torch.from_numpy(gen.bf16_bits_to_f32(b)).half().view(torch.int16).numpy().view(np.uint16)
+    return w, s, b
+
+
+def _t16(a, dt):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(TORCH16[dt])
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16])
+def test_dequantize_identity_scales(orc, bits, dt):
+    rng = np.random.default_rng(7)
+    q = rng.integers(0, 2 ** bits, size=(3, 128), dtype=np.uint32)
+    w = orc.pack(q, bits)
+    one = orc.from_f32(np.ones((3, 2), np.float32), dt)
+    zero = orc.from_f32(np.zeros((3, 2), np.float32), dt)
+    out = orc.to_f32(orc.dequantize(w, one, zero, 64, bits, dt), dt)
+    np.testing.assert_array_equal(out, q.astype(np.float32))
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("g", GROUPS)
+@pytest.mark.parametrize("dt", [O.F16, O.BF16])
+def test_dequantize_two_rounding_matches_torch_ops(orc, bits, g, dt):
+    w, s, b = _quant(100 + bits, 16, 256, bits, g, dt)
+    got = orc.dequantize(w, s, b, g, bits, dt)
+    q = torch.from_numpy(orc.unpack(w, bits).astype(np.float32)).to(TORCH16[dt])
+    st = _t16(s, dt).repeat_interleave(g, dim=1)
+    bt = _t16(b, dt).repeat_interleave(g, dim=1)
+    ref = (q * st) + bt  # torch rounds the product and the sum to the 16-bit type
+    np.testing.assert_array_equal(got, ref.view(torch.int16).numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("bits", (3, 4, 8))
+def test_dequantize_f32_no_fma(orc, bits):
+    w, s, b = _quant(5, 8, 128, bits, 32, O.F32)
+    got = orc.dequantize(w, s, b, 32, bits, O.F32)
+    q = orc.unpack(w, bits).astype(np.float32)
+    ref = (q * np.repeat(s, 32, axis=1)) + np.repeat(b, 32, axis=1)  # numpy: two roundings
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("dt", [O.F16, O.BF16])
+def test_dequantize_fused_single_rounding(orc, dt):
+    w, s, b = _quant(11, 16, 256, 4, 64, dt)
+    got = orc.dequantize(w, s, b, 64, 4, dt, fused=True)
+    q = orc.unpack(w, 4).astype(np.float64)
+    s64 = np.repeat(orc.to_f32(s, dt).astype(np.float64), 64, axis=1)
+    b64 = np.repeat(orc.to_f32(b, dt).astype(np.float64), 64, axis=1)
+    exact = q * s64 + b64
+    assert np.array_equal(exact.astype(np.float32).astype(np.float64), exact)  # float holds it
+    ref = torch.from_numpy(exact.astype(np.float32)).to(TORCH16[dt])
+    np.testing.assert_array_equal(got, ref.view(torch.int16).numpy().view(np.uint16))
+    # the two conventions do differ on these inputs, so the switch is meaningful
+    assert not np.array_equal(got, orc.dequantize(w, s, b, 64, 4, dt))
+
+
+# --- quantized matmul -------------------------------------------------------
+
+def _deq64(orc, w, s, b, g, bits, dt):
+    q = orc.unpack(w, bits).astype(np.float64)
+    sf = np.repeat(orc.to_f32(s, dt).astype(np.float64), g, axis=-1)
+    bf = np.repeat(orc.to_f32(b, dt).astype(np.float64), g, axis=-1)
+    return sf * q + bf
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+def test_qmm_f64_matches_numpy(orc, bits, dt):
+    M, N, K, g = 5, 48, 256, 64
+    w, s, b = _quant(21, N, K, bits, g, dt)
+    x = gen.np_x_bf16(3, (M, K))
+    y = orc.qmm_f64(x, O.BF16, w, s, b, dt, g, bits)
+    ref = gen.bf16_bits_to_f32(x).astype(np.float64) @ _deq64(orc, w, s, b, g, bits, dt).T
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("bits", (3, 4))
+def test_qmm_f64_no_transpose_matches_numpy(orc, bits):
+    M, N, K, g = 3, 128, 40, 32
+    w, s, b = _quant(22, K, N, bits, g, O.BF16)  # W stored [K, N], groups along N
+    x = gen.np_x_bf16(4, (M, K))
+    y = orc.qmm_f64(x, O.BF16, w, s, b, O.BF16, g, bits, transpose=False)
+    ref = gen.bf16_bits_to_f32(x).astype(np.float64) @ _deq64(orc, w, s, b, g, bits, O.BF16)
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_one_hot_reads_one_column(orc):
+    N, K, g, bits = 32, 128, 64, 4
+    w, s, b = _quant(23, N, K, bits, g, O.BF16)
+    deq = _deq64(orc, w, s, b, g, bits, O.BF16)
+    for k in (0, 7, 8, 63, 64, 127):
+        x = np.zeros((1, K), np.float32)
+        x[0, k] = 1.0
+        y = orc.qmm_f64(x, O.F32, w, s, b, O.BF16, g, bits)
+        np.testing.assert_array_equal(y[0], deq[:, k])
+
+
+def test_qmm_mlx_exact_on_integers_and_close_otherwise(orc):
+    N, K, g, bits = 16, 128, 32, 4
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint32)
+    w = orc.pack(q, bits)
+    one = orc.from_f32(np.ones((N, K // g), np.float32), O.BF16)
+    zero = orc.from_f32(np.zeros((N, K // g), np.float32), O.BF16)
+    x = orc.from_f32(rng.integers(-1, 2, size=(2, K)).astype(np.float32), O.BF16)
+    exact = orc.qmm_f64(x, O.BF16, w, one, zero, O.BF16, g, bits)
+    for b_ in (4, 3):  # the float-lane path and the bf16-accumulation path
+        wq = orc.pack(q % (2 ** b_), b_)
+        ex = orc.qmm_f64(x, O.BF16, wq, one, zero, O.BF16, g, b_)
+        got = orc.to_f32(orc.qmm_mlx(x, O.BF16, wq, one, zero, O.BF16, g, b_), O.BF16)
+        assert np.abs(ex).max() < 256  # every partial sum is a bf16 integer
+        np.testing.assert_array_equal(got, ex.astype(np.float32))
+    assert exact.shape == (2, N)
+    w, s, b = _quant(24, 64, 1024, 4, 64, O.BF16)
+    x = gen.np_x_bf16(5, (4, 1024))
+    ref = orc.qmm_f64(x, O.BF16, w, s, b, O.BF16, 64, 4)
+    got = orc.to_f32(orc.qmm_mlx(x, O.BF16, w, s, b, O.BF16, 64, 4), O.BF16)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-2
+
+
+# --- gather_qmm and the global sort ----------------------------------------
+
+def test_gather_matches_per_expert(orc):
+    # qwen3_next.rs:4344-4398: gather_qmm(x, W, [e]) == quantized_matmul(x, W[e])
+    E, N, K, g, bits = 4, 64, 64, 64, 4
+    w, s, b = _quant(30, N, K, bits, g, O.BF16)
+    w = np.stack([_quant(30 + e, N, K, bits, g, O.BF16)[0] for e in range(E)])
+    s = np.stack([_quant(30 + e, N, K, bits, g, O.BF16)[1] for e in range(E)])
+    b = np.stack([_quant(30 + e, N, K, bits, g, O.BF16)[2] for e in range(E)])
+    x = gen.np_x_bf16(6, (3, 1, K))
+    rhs = np.array([2, 0, 3], np.uint32)
+    y = orc.gather_qmm_f64(x, O.BF16, w, s, b, O.BF16, None, rhs, 1, N, K, g, bits)
+    for i, e in enumerate(rhs):
+        ref = orc.qmm_f64(x[i], O.BF16, w[e], s[e], b[e], O.BF16, g, bits)
+        np.testing.assert_array_equal(y[i], ref)
+    # null lhs with x batch 3 repeated: batch 6 -> x element i // 2
+    rhs6 = np.array([0, 1, 2, 3, 1, 0], np.uint32)
+    y6 = orc.gather_qmm_f64(x, O.BF16, w, s, b, O.BF16, None, rhs6, 1, N, K, g, bits)
+    lhs6 = np.array([0, 0, 1, 1, 2, 2], np.uint32)
+    y6e = orc.gather_qmm_f64(x, O.BF16, w, s, b, O.BF16, lhs6, rhs6, 1, N, K, g, bits)
+    np.testing.assert_array_equal(y6, y6e)
+    # out-of-range indices give NaN rows, in-range rows are untouched
+    bad = orc.gather_qmm_f64(x, O.BF16, w, s, b, O.BF16, np.array([0, 5], np.uint32),
+                             np.array([9, 1], np.uint32), 1, N, K, g, bits)
+    assert np.isnan(bad).all()
+    ok = orc.gather_qmm_f64(x, O.BF16, w, s, b, O.BF16, np.array([1], np.uint32),
+                            np.array([1], np.uint32), 1, N, K, g, bits)
+    np.testing.assert_array_equal(ok[0], orc.qmm_f64(x[1], O.BF16, w[1], s[1], b[1], O.BF16,
+                                                     g, bits))
+
+
+def test_gather_sort_is_stable_argsort(orc):
+    idx = gen.topk_routing(9, 64, 16, 4)
+    order, inv, srt, tok = orc.gather_sort(idx, 4)
+    flat = idx.reshape(-1)
+    np.testing.assert_array_equal(order, np.argsort(flat, kind="stable"))
+    np.testing.assert_array_equal(srt, flat[order])
+    assert np.all(np.diff(srt.astype(np.int64)) >= 0)
+    np.testing.assert_array_equal(inv[order], np.arange(flat.size))
+    np.testing.assert_array_equal(tok, order // 4)
+
+
+def test_topk_routing_rows_are_distinct_experts():
+    idx = gen.topk_routing(1, 512, 128, 8)
+    assert idx.shape == (512, 8) and idx.max() < 128
+    assert all(len(set(r)) == 8 for r in idx.tolist())
+
+
+def test_swiglu_matches_torch_silu(orc):
+    g = gen.np_x_bf16(1, (4096,))
+    u = gen.np_x_bf16(2, (4096,))
+    got = orc.swiglu(g, u, O.BF16)
+    gt = torch.from_numpy(gen.bf16_bits_to_f32(g).astype(np.float64))
+    ut = torch.from_numpy(gen.bf16_bits_to_f32(u).astype(np.float64))
+    ref64 = (torch.nn.functional.silu(gt) * ut).numpy()
+    ref = orc.from_f32(ref64.astype(np.float32), O.BF16)
+    # rounding double -> bf16 directly vs via float can differ only at exact ties
+    assert (got != ref).sum() <= 2
+    zero = orc.swiglu(np.zeros(4, np.uint16), u[:4], O.BF16)
+    assert gen.bf16_bits_to_f32(zero).tolist() == [0.0] * 4  # +-0: sign follows u
+
+
+def test_splitmix64_published_vector():
+    # SplitMix64 reference output for seed 1234567 (Vigna's splitmix64.c)
+    assert [int(v) for v in gen.splitmix64(1234567, 5)] == [
+        6457827717110365317, 3203168211198807973, 9817491932198370423,
+        4593380528125082431, 16408922859458223821]
+    assert [int(v) for v in gen.splitmix64(1234567, 2, offset=3)] == [
+        4593380528125082431, 16408922859458223821]
