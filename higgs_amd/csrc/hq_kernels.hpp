@@ -49,6 +49,7 @@ struct DeqArgs {
 #define HQ_DECLARE_LAUNCHERS(B)                          \
   hipError_t launch_dequant_b##B(const DeqArgs& a);      \
   hipError_t launch_qmv_t_b##B(const QArgs& a);          \
+  hipError_t launch_qmvx_t_b##B(const QArgs& a);         \
   hipError_t launch_qmm_t_b##B(const QArgs& a);          \
   hipError_t launch_qmv_n_b##B(const QArgs& a);
 

@@ -1,0 +1,707 @@
+// hq_qmvx.hip -- matrix-core GEMV for decode (M <= 8 rows of x, x in bf16 or
+// fp16), one bit width (HQ_BITS).
+//
+// y[m, n] = sum_k x[m, k] * (s[n, g] * q[n, k] + b[n, g]),  g = k / group_size
+// (mlx-rs ops::quantized_matmul, transpose=true, as called from
+// crates/higgs-models/src/qwen3_next.rs:218-227; LSB-first packing and group
+// math as stated in-tree at qwen3_next.rs:969-988).
+//
+// Why MFMA for a GEMV: at 8 TB/s a 4-bit weight stream is 16 G elements/s,
+// and a scalar dequantize-multiply-add path needs ~3 VALU ops per element --
+// more than the 39 T lane-ops/s the VALU has. Here the VALU only turns each
+// u32 of nibbles into four (OFF + q) bf16 pairs with one AND-OR each
+// (0.875 ops per element); the matrix cores do the multiply-add.
+//
+// Layout of one v_mfma_f32_16x16x32 step: B = 16 weight rows (n = lane % 16)
+// x 32 k, A = x rows, D[m', n] in fp32. A wave walks 128-element "segments"
+// of K: lane (n, q = lane / 16) loads pack q (32 elements, HQ_BITS words) of
+// row n, and its four words feed four MFMA steps. Within a segment the packs
+// of one lane group belong to group-half h = q * Z / 4 (Z = 128 / group_size
+// groups per segment), and A row m' = 4h + m (8h + m when M > 4) carries x[m]
+// only in the k-blocks of half h, zeros elsewhere. One MFMA therefore yields
+// the per-group partial dot products for every (m, h) without mixing groups,
+// and the epilogue applies  s * D + (b - OFF * s) * X  with X = sum of x over
+// the group (the OFF term removes the exponent bias baked into OFF + q).
+//
+// x is staged once per block in LDS (row-major, each 8-element block stored in
+// the MFMA pair order (0,4,1,5,2,6,3,7)), with a zero row that A lanes of other
+// halves read; X sums are computed during staging. Waves of a block split K
+// into contiguous segment ranges; partial sums are reduced through LDS in a
+// fixed order (deterministic).
+#include "hq_common.hpp"
+#include "hq_kernels.hpp"
+
+#ifndef HQ_BITS
+#error "compile with -DHQ_BITS=<2|3|4|5|6|8>"
+#endif
+
+namespace hq {
+
+namespace {
+
+struct QXKern {
+  void* y;
+  const void* x;
+  const uint32_t* w;
+  const void* s;
+  const void* b;
+  const uint32_t* lhs;
+  const uint32_t* rhs;
+  int64_t batch, x_rep, x_batch, w_batch;
+  int M, N, K;
+  int KC;       // K elements staged per chunk (multiple of 128)
+  int S;        // segments per wave per chunk
+};
+
+template <int XDT> struct XMma;
+template <> struct XMma<DT_BF16> {
+  using frag = bf16x8;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  // bf16 128.0 in both halves: (0x4300 | q) == 128 + q exactly for q < 128.
+  static constexpr uint32_t OFFB = 0x43004300u;
+  static constexpr float OFF = 128.f;
+};
+template <> struct XMma<DT_F16> {
+  using frag = f16x8;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  // fp16 1024.0: (0x6400 | q) == 1024 + q exactly for q < 1024.
+  static constexpr uint32_t OFFB = 0x64006400u;
+  static constexpr float OFF = 1024.f;
+};
+
+// 8-bit weights with bf16 x: 128 + q does not fit bf16's 8-bit significand,
+// so q is converted exactly (q <= 255 is a bf16 integer) and OFF is 0.
+template <int BITS, int XDT>
+constexpr bool kExact8 = (BITS == 8 && XDT == DT_BF16);
+
+// Step i (0..3) of a 32-element pack: four u32, each two 16-bit MFMA operand
+// values, element order (8i+j, 8i+j+4) for j = 0..3.
+template <int BITS, int XDT>
+__device__ __forceinline__ u32x4 unpack_step(const uint32_t (&wd)[BITS], int i) {
+  u32x4 r;
+  if constexpr (BITS == 4) {
+    const uint32_t w = wd[i];
+    r[0] = (w & 0x000F000Fu) | XMma<XDT>::OFFB;
+    r[1] = ((w >> 4) & 0x000F000Fu) | XMma<XDT>::OFFB;
+    r[2] = ((w >> 8) & 0x000F000Fu) | XMma<XDT>::OFFB;
+    r[3] = ((w >> 12) & 0x000F000Fu) | XMma<XDT>::OFFB;
+  } else if constexpr (kExact8<BITS, XDT>) {
+    const uint32_t lo = wd[2 * i], hi = wd[2 * i + 1];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t fa = __float_as_uint((float)((lo >> (8 * j)) & 0xffu));
+      const uint32_t fb = __float_as_uint((float)((hi >> (8 * j)) & 0xffu));
+      r[j] = (fa >> 16) | (fb & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t qa = pack_elem<BITS>(wd, 8 * i + j);
+      const uint32_t qb = pack_elem<BITS>(wd, 8 * i + j + 4);
+      r[j] = (qa | (qb << 16)) | XMma<XDT>::OFFB;
+    }
+  }
+  return r;
+}
+
+template <int ODT>
+__device__ __forceinline__ st_t<ODT> nanv() {
+  if constexpr (ODT == DT_F32) return __uint_as_float(0x7fc00000u);
+  else if constexpr (ODT == DT_BF16) return (uint16_t)0x7fc0u;
+  else return (uint16_t)0x7e00u;
+}
+
+constexpr int kU = 4;  // segments whose loads are issued together
+
+// BITS, x dtype (bf16 | fp16), scale dtype, MB = M rounded up to 1/2/4/8,
+// GS = group size.
+template <int BITS, int XDT, int SDT, int MB, int GS>
+__global__ __launch_bounds__(1024) void qmvx_kernel(QXKern a) {
+  using XS = st_t<XDT>;
+  using SS = st_t<SDT>;
+  constexpr int ODT = result_dtype(XDT, SDT);
+  using OS = st_t<ODT>;
+  using T = XMma<XDT>;
+  constexpr float OFF = kExact8<BITS, XDT> ? 0.f : T::OFF;
+  constexpr int Z = 128 / GS;                    // groups per segment
+  constexpr int RPH = MB <= 4 ? 4 : 8;           // A rows per group-half
+  constexpr int NMF = (Z * RPH + 15) / 16;       // MFMAs per step
+  constexpr int HPM = 16 / RPH;                  // halves per MFMA
+  constexpr int VM = MB < 4 ? MB : 4;            // useful D values per lane
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int W = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int M = a.M, N = a.N, K = a.K, KC = a.KC;
+  const int n0 = blockIdx.x * 16;
+  const int packs = K >> 5;
+  const int64_t P = (int64_t)packs * BITS;  // words per weight row
+  const int64_t G = K / GS;
+
+  // LDS: x rows [M + 1][KC] (row M is zeros), X sums [KC/GS][RPH] floats,
+  // reduction slots [W][Z][M][16] floats.
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  float* Xs = reinterpret_cast<float*>(smem + (size_t)(M + 1) * KC * 2);
+  float* red = Xs + (KC / GS) * RPH;
+
+  const int nl = lane & 15, q = lane >> 4;
+  const int n_eff = min(n0 + nl, N - 1);
+
+  // Per-lane A-operand base (bytes into xs) for each MFMA of a step.
+  int abase[NMF];
+#pragma unroll
+  for (int mf = 0; mf < NMF; mf++) {
+    const int mrow = nl;                            // A row m' of this lane
+    const int h = mf * HPM + mrow / RPH;            // group-half of that row
+    const int m = mrow % RPH;
+    const int hq = q * Z / 4;                       // half of this lane's k-block
+    const bool valid = (h == hq) && (m < M) && (h < Z);
+    abase[mf] = (valid ? m : M) * KC * 2 + q * 64;
+  }
+  // D-side: half and x-row of this lane's accumulator values, per MFMA.
+  int dh[NMF];
+#pragma unroll
+  for (int mf = 0; mf < NMF; mf++) dh[mf] = mf * HPM + (MB <= 4 ? q : q / 2);
+  const int dm0 = MB <= 4 ? 0 : 4 * (q & 1);  // x row of value v is dm0 + v
+
+  for (int64_t bi = blockIdx.y; bi < a.batch; bi += gridDim.y) {
+    const int64_t xi = a.lhs ? (int64_t)a.lhs[bi] : bi / a.x_rep;
+    const int64_t wi = a.rhs ? (int64_t)a.rhs[bi] : 0;
+    OS* yb = (OS*)a.y + bi * (int64_t)M * N;
+    if (xi >= a.x_batch || wi >= a.w_batch) {
+      for (int t = tid; t < M * 16; t += blockDim.x)
+        if (n0 + (t & 15) < N) yb[(int64_t)(t >> 4) * N + n0 + (t & 15)] = nanv<ODT>();
+      continue;
+    }
+    const XS* xb = (const XS*)a.x + xi * (int64_t)M * K;
+    const uint32_t* wrow = a.w + wi * (int64_t)N * P + (int64_t)n_eff * P;
+    const SS* srow = (const SS*)a.s + wi * (int64_t)N * G + (int64_t)n_eff * G;
+    const SS* brow = (const SS*)a.b + wi * (int64_t)N * G + (int64_t)n_eff * G;
+
+    float acc[NMF][4];
+#pragma unroll
+    for (int mf = 0; mf < NMF; mf++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) acc[mf][v] = 0.f;
+
+    for (int kc0 = 0; kc0 < K; kc0 += KC) {
+      const int kcn = min(KC, K - kc0);          // elements in this chunk
+      const int nseg = (kcn + 127) >> 7;
+      const int seg_lo = min(wv * a.S, nseg);
+      const int seg_hi = min(seg_lo + a.S, nseg);
+
+      // ---- stage x chunk + group sums ----
+      {
+        const int cpr = KC >> 3;                  // 8-element blocks per row
+        for (int t = tid; t < (M + 1) * cpr; t += blockDim.x) {
+          const int m = t / cpr, c = t - m * cpr;
+          const int k = kc0 + c * 8;
+          u32x4 d = {0u, 0u, 0u, 0u};
+          float sum = 0.f;
+          if (m < M && k < K) {
+            d = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * K + k);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              sum += DT_<XDT>::to_f32((uint16_t)(d[e] & 0xffffu)) +
+                     DT_<XDT>::to_f32((uint16_t)(d[e] >> 16));
+          }
+          u32x4 o;
+          o[0] = (d[0] & 0xffffu) | (d[2] << 16);
+          o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
+          o[2] = (d[1] & 0xffffu) | (d[3] << 16);
+          o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
+          *reinterpret_cast<u32x4*>(xs + (size_t)m * KC + c * 8) = o;
+          // GS/8 consecutive threads hold one group: reduce in the wave.
+#pragma unroll
+          for (int o2 = 1; o2 < GS / 8; o2 <<= 1) sum += __shfl_xor(sum, o2, 64);
+          if (m < M && (c & (GS / 8 - 1)) == 0) Xs[(c / (GS / 8)) * RPH + m] = sum;
+        }
+        for (int t = tid; t < (KC / GS) * RPH; t += blockDim.x)
+          if ((t % RPH) >= M) Xs[t] = 0.f;
+      }
+      __syncthreads();
+
+      // ---- stream this wave's segments ----
+      for (int sb = seg_lo; sb < seg_hi; sb += kU) {
+        uint32_t wd[kU][BITS];
+        float sv[kU][NMF], bv[kU][NMF];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+          const int seg = sb + u;
+          const int p = ((kc0 >> 7) + seg) * 4 + q;  // pack index in the row
+          if (seg < seg_hi && p < packs) {
+            load_pack<BITS>(wrow + (int64_t)p * BITS, wd[u]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < BITS; i++) wd[u][i] = 0u;
+          }
+#pragma unroll
+          for (int mf = 0; mf < NMF; mf++) {
+            const int hc = min(dh[mf], Z - 1);
+            int64_t g = (int64_t)((kc0 >> 7) + seg) * Z + hc;
+            g = min(g, G - 1);
+            sv[u][mf] = DT_<SDT>::load(srow, g);
+            bv[u][mf] = DT_<SDT>::load(brow, g);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+          // Segments past this wave's range (tail batch) are computed on a
+          // clamped in-range address and contribute zero.
+          const bool live = sb + u < seg_hi;
+          const int seg = min(sb + u, nseg - 1);
+          floatx4 d[NMF];
+#pragma unroll
+          for (int mf = 0; mf < NMF; mf++) d[mf] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const u32x4 bw = unpack_step<BITS, XDT>(wd[u], i);
+#pragma unroll
+            for (int mf = 0; mf < NMF; mf++) {
+              const u32x4 av = *reinterpret_cast<const u32x4*>(
+                  reinterpret_cast<const unsigned char*>(xs) + abase[mf] + seg * 256 + i * 16);
+              d[mf] = T::mma(__builtin_bit_cast(typename T::frag, av),
+                             __builtin_bit_cast(typename T::frag, bw), d[mf]);
+            }
+          }
+#pragma unroll
+          for (int mf = 0; mf < NMF; mf++) {
+            const int hc = min(dh[mf], Z - 1);
+            const float s = live ? sv[u][mf] : 0.f;
+            const float bo = live ? fmaf(-OFF, sv[u][mf], bv[u][mf]) : 0.f;
+            const floatx4 X = *reinterpret_cast<const floatx4*>(Xs + (seg * Z + hc) * RPH + dm0);
+#pragma unroll
+            for (int v = 0; v < VM; v++) acc[mf][v] = fmaf(s, d[mf][v], fmaf(bo, X[v], acc[mf][v]));
+          }
+        }
+      }
+      __syncthreads();  // xs / Xs are restaged by the next chunk
+    }
+
+    // ---- reduce over waves and halves, fixed order ----
+#pragma unroll
+    for (int mf = 0; mf < NMF; mf++) {
+      const int h = dh[mf];
+      if (h < Z) {
+#pragma unroll
+        for (int v = 0; v < VM; v++) {
+          const int m = dm0 + v;
+          if (m < M) red[((wv * Z + h) * M + m) * 16 + nl] = acc[mf][v];
+        }
+      }
+    }
+    __syncthreads();
+    for (int t = tid; t < M * 16; t += blockDim.x) {
+      const int m = t >> 4, n = t & 15;
+      float r = 0.f;
+      for (int w2 = 0; w2 < W; w2++)
+#pragma unroll
+        for (int h = 0; h < Z; h++) r += red[((w2 * Z + h) * M + m) * 16 + n];
+      if (n0 + n < N) yb[(int64_t)m * N + n0 + n] = DT_<ODT>::from_f32(r);
+    }
+    __syncthreads();  // red is rewritten by the next batch element
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent variant for one product (batch == 1) of exact shape
+// (K % 1024 == 0): x is staged once per block, the block walks row tiles
+// t = blockIdx.x + j * gridDim.x, and each tile is split into R rounds of W
+// waves x S segments. A wave's S segments of a round share MFMA accumulators:
+// segment u, group-half h, x row m goes to A row ((u % SU) * Z + h) * MB + m,
+// so up to 16 / (Z * MB) segments fill one 16-row accumulator and the scale
+// epilogue runs once per accumulator instead of once per segment. The loads
+// of the next round (possibly of the next tile) are in flight while the
+// current one is computed (register double buffer). Partials of a tile meet
+// in LDS after one block barrier (double-buffered slots, fixed-order sum).
+// ---------------------------------------------------------------------------
+
+struct PKern {
+  void* y;
+  const void* x;
+  const uint32_t* w;
+  const void* s;
+  const void* b;
+  int M, N, K;
+  int R;        // rounds per tile
+  int ntiles;   // ceil(N / 16)
+  // 0x000F000F and the operand offset pair, passed as kernel arguments so the
+  // compiler keeps them in registers and emits one v_and_or_b32 per pair (gfx9
+  // VOP3 cannot encode 32-bit literals).
+  uint32_t nib_mask, off_pair;
+};
+
+// NG consecutive scale values as floats (vector load).
+template <int SDT, int NG>
+__device__ __forceinline__ void load_groups(const st_t<SDT>* p, float (&o)[NG]) {
+  if constexpr (SDT == DT_F32) {
+    if constexpr (NG == 4) {
+      const float4 v = *reinterpret_cast<const float4*>(p);
+      o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    } else if constexpr (NG == 2) {
+      const float2 v = *reinterpret_cast<const float2*>(p);
+      o[0] = v.x; o[1] = v.y;
+    } else {
+      o[0] = p[0];
+    }
+  } else {
+    if constexpr (NG == 4) {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+      o[0] = DT_<SDT>::to_f32((uint16_t)(v[0] & 0xffffu));
+      o[1] = DT_<SDT>::to_f32((uint16_t)(v[0] >> 16));
+      o[2] = DT_<SDT>::to_f32((uint16_t)(v[1] & 0xffffu));
+      o[3] = DT_<SDT>::to_f32((uint16_t)(v[1] >> 16));
+    } else if constexpr (NG == 2) {
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+      o[0] = DT_<SDT>::to_f32((uint16_t)(v & 0xffffu));
+      o[1] = DT_<SDT>::to_f32((uint16_t)(v >> 16));
+    } else {
+      o[0] = DT_<SDT>::to_f32(p[0]);
+    }
+  }
+}
+
+template <int BITS, int XDT, int SDT, int MB, int GS, int S>
+struct PCfg {
+  static constexpr int Z = 128 / GS;                 // groups per segment
+  static constexpr int SU = (16 / (Z * MB)) < S ? (16 / (Z * MB)) : S;  // segs per acc
+  static constexpr int NB = S / SU;                  // accumulators per round
+  static constexpr int NSLOT = SU * Z;               // (segment, half) slots used
+  static constexpr int NG = MB >= 4 ? 1 : 4 / MB;    // groups per lane per acc
+  static_assert(Z * MB <= 16, "x rows x group-halves must fit 16 MFMA rows");
+  static_assert(S % SU == 0, "segments per round must fill whole accumulators");
+};
+
+template <int BITS, int XDT, int SDT, int MB, int GS, int S>
+struct RoundRegs {
+  using C = PCfg<BITS, XDT, SDT, MB, GS, S>;
+  uint32_t wd[S][BITS];
+  float sv[C::NB][C::NG], bv[C::NB][C::NG];
+};
+
+template <int BITS, int XDT, int SDT, int MB, int GS, int S>
+__global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
+  using C = PCfg<BITS, XDT, SDT, MB, GS, S>;
+  using XS = st_t<XDT>;
+  using SS = st_t<SDT>;
+  constexpr int ODT = result_dtype(XDT, SDT);
+  using OS = st_t<ODT>;
+  using T = XMma<XDT>;
+  using Regs = RoundRegs<BITS, XDT, SDT, MB, GS, S>;
+  constexpr float OFF = kExact8<BITS, XDT> ? 0.f : T::OFF;
+  constexpr int Z = C::Z, SU = C::SU, NB = C::NB, NSLOT = C::NSLOT, NG = C::NG;
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int W = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int M = a.M, N = a.N, K = a.K, R = a.R;
+  const int Kp = K;                       // exact: K % 1024 == 0
+  const int64_t P = (int64_t)(K >> 5) * BITS;
+  const int64_t G = K / GS;
+
+  // LDS: x rows [M][K] | 64 B of zeros | X sums [G][MB] | red [2][W][64][4]
+  const int zoff = M * K * 2;
+  float* Xs = reinterpret_cast<float*>(smem + zoff + 64);
+  float* red = Xs + G * MB;
+
+  const int nl = lane & 15, q = lane >> 4;
+  // A side: this lane supplies x row mA of slot sigA for k-block q.
+  const int sigA = nl / MB, mA = nl % MB;
+  const int uA = sigA / Z, hA = sigA % Z;
+  const bool validA = (hA == q * Z / 4) && (mA < M) && (sigA < NSLOT);
+  const int xlane = mA * K * 2 + q * 64;
+  // D side: values v = 0..3 of this lane are rows 4q + v.
+  const int sig0 = (4 * q) / MB;          // slot of value 0
+  const int gsig = sig0 < NSLOT ? sig0 : 0;  // clamped for loads
+  const int md0 = MB >= 8 ? 4 * (q & 1) : 0;
+
+  // The offset goes through a VGPR (a plain v_mov, no hazards) so that the
+  // mask is the AND-OR's only scalar operand (gfx9 VOP3 reads at most one).
+  const uint32_t mask_s = a.nib_mask;
+  uint32_t off_v;
+  asm("v_mov_b32 %0, %1" : "=v"(off_v) : "s"(a.off_pair));
+
+  auto unpack = [&](const uint32_t (&wd)[BITS], int i) -> u32x4 {
+    if constexpr (BITS == 4) {
+      const uint32_t w = wd[i];
+      u32x4 r;
+      r[0] = (w & mask_s) | off_v;
+      r[1] = ((w >> 4) & mask_s) | off_v;
+      r[2] = ((w >> 8) & mask_s) | off_v;
+      r[3] = ((w >> 12) & mask_s) | off_v;
+      return r;
+    } else {
+      return unpack_step<BITS, XDT>(wd, i);
+    }
+  };
+
+  auto issue = [&](Regs& r, int t, int rnd) {
+    const int n = min(t * 16 + nl, N - 1);
+    const int seg_base = (rnd * W + wv) * S;
+    const uint32_t* wp = a.w + (int64_t)n * P + (int64_t)(seg_base * 4 + q) * BITS;
+#pragma unroll
+    for (int u = 0; u < S; u++) load_pack<BITS>(wp + u * 4 * BITS, r.wd[u]);
+    const SS* sp = (const SS*)a.s + (int64_t)n * G + seg_base * Z + gsig;
+    const SS* bp = (const SS*)a.b + (int64_t)n * G + seg_base * Z + gsig;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      load_groups<SDT, NG>(sp + j * NSLOT, r.sv[j]);
+      load_groups<SDT, NG>(bp + j * NSLOT, r.bv[j]);
+    }
+  };
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const Regs& r, int rnd) {
+    const int seg_base = (rnd * W + wv) * S;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      // the one segment of this accumulator whose A rows this lane fills
+      const int real = xlane + (seg_base + j * SU + uA) * 256;
+      floatx4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int uu = 0; uu < SU; uu++) {
+        const int addr = (validA && uA == uu) ? real : zoff;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const u32x4 bw = unpack(r.wd[j * SU + uu], i);
+          const u32x4 av = *reinterpret_cast<const u32x4*>(smem + addr + i * 16);
+          d = T::mma(__builtin_bit_cast(typename T::frag, av),
+                     __builtin_bit_cast(typename T::frag, bw), d);
+        }
+      }
+      const int g0 = seg_base * Z + j * NSLOT + gsig;
+      const floatx4 X = *reinterpret_cast<const floatx4*>(Xs + g0 * MB + md0);
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int gi = NG == 4 ? v : (NG == 2 ? v / 2 : 0);
+        const float s = r.sv[j][gi];
+        const float bo = fmaf(-OFF, s, r.bv[j][gi]);
+        acc[v] = fmaf(s, d[v], fmaf(bo, X[v], acc[v]));
+      }
+    }
+  };
+
+  auto finish_tile = [&](int t, int buf) {
+    float* rb = red + buf * (W * 256);
+    *reinterpret_cast<floatx4*>(rb + (wv * 64 + lane) * 4) = floatx4{acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+    for (int v = 0; v < 4; v++) acc[v] = 0.f;
+    __syncthreads();
+    for (int e = tid; e < M * 16; e += blockDim.x) {
+      const int m = e >> 4, n = e & 15;
+      float sum = 0.f;
+      for (int w2 = 0; w2 < W; w2++)
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++)
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            const int mp = 4 * qq + v;
+            if (mp % MB == m && mp / MB < NSLOT) sum += rb[(w2 * 64 + qq * 16 + n) * 4 + v];
+          }
+      if (t * 16 + n < N) ((OS*)a.y)[(int64_t)m * N + t * 16 + n] = DT_<ODT>::from_f32(sum);
+    }
+  };
+
+  Regs r0, r1;
+  const int step = gridDim.x;
+  int t = blockIdx.x, rnd = 0;
+  issue(r0, t, 0);
+
+  // ---- stage x + group sums (all threads) ----
+  {
+    const XS* xb = (const XS*)a.x;
+    const int cpr = K >> 3;
+    for (int e = tid; e < M * cpr; e += blockDim.x) {
+      const int m = e / cpr, c = e - m * cpr;
+      const int k = c * 8;
+      const u32x4 d = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * K + k);
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        sum += DT_<XDT>::to_f32((uint16_t)(d[j] & 0xffffu)) + DT_<XDT>::to_f32((uint16_t)(d[j] >> 16));
+      u32x4 o;
+      o[0] = (d[0] & 0xffffu) | (d[2] << 16);
+      o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
+      o[2] = (d[1] & 0xffffu) | (d[3] << 16);
+      o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
+      *reinterpret_cast<u32x4*>(smem + ((size_t)m * K + k) * 2) = o;
+#pragma unroll
+      for (int o2 = 1; o2 < GS / 8; o2 <<= 1) sum += __shfl_xor(sum, o2, 64);
+      if ((c & (GS / 8 - 1)) == 0) Xs[(c / (GS / 8)) * MB + m] = sum;
+    }
+    for (int e = tid; e < G * MB; e += blockDim.x)
+      if ((e % MB) >= M) Xs[e] = 0.f;
+    if (tid < 4) reinterpret_cast<u32x4*>(smem + zoff)[tid] = u32x4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+
+  // items (t, rnd) in order; buffers alternate, the next item's loads are
+  // issued before the current item is computed
+  int buf = 0;
+  while (true) {
+    if (t >= a.ntiles) break;
+    int t1 = t, r1n = rnd + 1;
+    if (r1n == R) { r1n = 0; t1 += step; }
+    if (t1 < a.ntiles) issue(r1, t1, r1n);
+    compute(r0, rnd);
+    if (rnd == R - 1) { finish_tile(t, buf); buf ^= 1; }
+    t = t1; rnd = r1n;
+    if (t >= a.ntiles) break;
+    t1 = t; r1n = rnd + 1;
+    if (r1n == R) { r1n = 0; t1 += step; }
+    if (t1 < a.ntiles) issue(r0, t1, r1n);
+    compute(r1, rnd);
+    if (rnd == R - 1) { finish_tile(t, buf); buf ^= 1; }
+    t = t1; rnd = r1n;
+  }
+}
+
+int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      cus = v;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+// Launches the persistent kernel, or returns hipErrorNotSupported for shapes
+// it does not take (the caller then uses the blocked kernel).
+template <int XDT, int SDT, int MB, int GS, int S>
+hipError_t run_qmvp_s(const QArgs& a, int W, int R) {
+  using C = PCfg<HQ_BITS, XDT, SDT, MB, GS, S>;
+  const size_t G = (size_t)a.K / GS;
+  const size_t lds = (size_t)a.M * a.K * 2 + 64 + G * MB * 4 + (size_t)2 * W * 256 * 4;
+  if (lds > 160 * 1024) return hipErrorNotSupported;
+  PKern k;
+  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
+  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K; k.R = R;
+  k.nib_mask = 0x000F000Fu;
+  k.off_pair = XMma<XDT>::OFFB;
+  const int ntiles = (int)((a.N + 15) / 16);
+  k.ntiles = ntiles;
+  const int per_cu = lds > 80 * 1024 ? 1 : 2;
+  const int maxb = per_cu * device_cus();
+  const int per = (ntiles + maxb - 1) / maxb;
+  const int grid = (ntiles + per - 1) / per;
+  auto fn = qmvp_kernel<HQ_BITS, XDT, SDT, MB, GS, S>;
+  static bool big_lds = false;
+  if (lds > 64 * 1024 && !big_lds) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    big_lds = true;
+  }
+  (void)sizeof(C);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, a.stream, k);
+  return hipGetLastError();
+}
+
+template <int XDT, int SDT, int MB, int GS>
+hipError_t run_qmvp(const QArgs& a) {
+  constexpr int Z = 128 / GS;
+  if constexpr (Z * MB > 16) {
+    return hipErrorNotSupported;
+  } else {
+    if (a.K % 1024 != 0) return hipErrorNotSupported;
+    const int nseg = (int)(a.K / 128);
+    const int ntiles = (int)((a.N + 15) / 16);
+    // S = 8 segments per round; W waves such that W * 8 divides nseg, as many
+    // as fit 8 (more waves per tile when there are few tiles).
+    int W = 0;
+    const int wmax = 8;
+    for (int c = wmax; c >= 1; c--)
+      if ((nseg / 8) % c == 0) { W = c; break; }
+    if (W == 0) return hipErrorNotSupported;
+    return run_qmvp_s<XDT, SDT, MB, GS, 8>(a, W, nseg / (8 * W));
+  }
+}
+
+template <int XDT, int SDT, int MB, int GS>
+hipError_t run_qmvx(const QArgs& a) {
+  QXKern k;
+  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
+  k.lhs = a.lhs; k.rhs = a.rhs;
+  k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
+  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
+  constexpr int RPH = MB <= 4 ? 4 : 8;
+  constexpr int Z = 128 / GS;
+  const int kpad = (int)((a.K + 127) / 128 * 128);
+  // x chunk: at most ~40 KB of bf16 rows (+ zero row) so two blocks fit a CU.
+  int kc = (40960 / ((int)a.M + 1)) / 128 * 128;
+  if (kc < 128) kc = 128;
+  if (kc > kpad) kc = kpad;
+  k.KC = kc;
+  const int nseg = kc / 128;
+  int W = (nseg + kU - 1) / kU;
+  if (W > 16) W = 16;
+  if (W < 1) W = 1;
+  k.S = (nseg + W - 1) / W;
+  const size_t lds = (size_t)(a.M + 1) * kc * 2 + (size_t)(kc / GS) * RPH * 4 +
+                     (size_t)W * Z * a.M * 16 * 4;
+  dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)(a.batch < 65535 ? a.batch : 65535));
+  auto fn = qmvx_kernel<HQ_BITS, XDT, SDT, MB, GS>;
+  static bool big_lds = false;  // opt-in to > 64 KB once per instantiation
+  if (lds > 64 * 1024 && !big_lds) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    big_lds = true;
+  }
+  hipLaunchKernelGGL(fn, grid, dim3(64 * W), lds, a.stream, k);
+  return hipGetLastError();
+}
+
+template <int XDT, int SDT, int MB, int GS>
+hipError_t run_qmvx_any(const QArgs& a) {
+  if (a.batch == 1 && !a.lhs && !a.rhs) {
+    hipError_t e = run_qmvp<XDT, SDT, MB, GS>(a);
+    if (e != hipErrorNotSupported) return e;
+  }
+  return run_qmvx<XDT, SDT, MB, GS>(a);
+}
+
+template <int XDT, int SDT, int MB>
+hipError_t run_qmvx_g(const QArgs& a) {
+  switch (a.group_size) {
+    case 32: return run_qmvx_any<XDT, SDT, MB, 32>(a);
+    case 64: return run_qmvx_any<XDT, SDT, MB, 64>(a);
+    default: return run_qmvx_any<XDT, SDT, MB, 128>(a);
+  }
+}
+
+template <int XDT, int SDT>
+hipError_t run_qmvx_m(const QArgs& a) {
+  if (a.M <= 1) return run_qmvx_g<XDT, SDT, 1>(a);
+  if (a.M <= 2) return run_qmvx_g<XDT, SDT, 2>(a);
+  if (a.M <= 4) return run_qmvx_g<XDT, SDT, 4>(a);
+  return run_qmvx_g<XDT, SDT, 8>(a);
+}
+
+}  // namespace
+
+#define HQ_CAT_(a, b) a##b
+#define HQ_CAT(a, b) HQ_CAT_(a, b)
+
+hipError_t HQ_CAT(launch_qmvx_t_b, HQ_BITS)(const QArgs& a) {
+  switch (a.xdt * 3 + a.sdt) {
+    case DT_BF16 * 3 + DT_BF16: return run_qmvx_m<DT_BF16, DT_BF16>(a);
+    case DT_BF16 * 3 + DT_F16: return run_qmvx_m<DT_BF16, DT_F16>(a);
+    case DT_BF16 * 3 + DT_F32: return run_qmvx_m<DT_BF16, DT_F32>(a);
+    case DT_F16 * 3 + DT_F16: return run_qmvx_m<DT_F16, DT_F16>(a);
+    case DT_F16 * 3 + DT_BF16: return run_qmvx_m<DT_F16, DT_BF16>(a);
+    case DT_F16 * 3 + DT_F32: return run_qmvx_m<DT_F16, DT_F32>(a);
+    default: return hipErrorInvalidValue;  // fp32 x uses the VALU kernel
+  }
+}
+
+}  // namespace hq
