@@ -403,7 +403,7 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
   const int64_t P = (int64_t)(K >> 5) * BITS;
   const int64_t G = K / GS;
 
-  // LDS: x rows [M][K] | 64 B of zeros | X sums [G][MB] | red [2][W][64][4]
+  // LDS: x rows [M][K] | 64 B of zeros | X sums [G][MB] | red [2][W][MB][16]
   const int zoff = M * K * 2;
   float* Xs = reinterpret_cast<float*>(smem + zoff + 64);
   float* red = Xs + G * MB;
@@ -486,23 +486,48 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
     }
   };
 
+  // Per-lane value v is x row (4q+v) % MB of slot (4q+v) / MB; slots past
+  // NSLOT hold no segment and are dropped.
+  float keep[4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) keep[v] = ((4 * q + v) / MB < NSLOT) ? 1.f : 0.f;
+  constexpr int MV = MB < 4 ? MB : 4;  // distinct x rows per lane
+
   auto finish_tile = [&](int t, int buf) {
-    float* rb = red + buf * (W * 256);
-    *reinterpret_cast<floatx4*>(rb + (wv * 64 + lane) * 4) = floatx4{acc[0], acc[1], acc[2], acc[3]};
+    // 1) fold this lane's values onto its x rows, 2) sum over the lane groups
+    //    that hold other slots of the same rows, 3) one LDS slot per wave.
+    float part[MV];
+#pragma unroll
+    for (int j = 0; j < MV; j++) part[j] = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) part[v % MV] += keep[v] * acc[v];
 #pragma unroll
     for (int v = 0; v < 4; v++) acc[v] = 0.f;
+    if constexpr (MB < 8) {
+#pragma unroll
+      for (int j = 0; j < MV; j++) {
+        part[j] += __shfl_xor(part[j], 16, 64);
+        part[j] += __shfl_xor(part[j], 32, 64);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < MV; j++) part[j] += __shfl_xor(part[j], 32, 64);
+    }
+    float* rb = red + buf * (W * 16 * MB);
+    // rows held by lane group q after the folds: q == 0 has rows 0..MV-1; for
+    // MB == 8, q == 1 has rows 4..7.
+    if (q == 0 || (MB == 8 && q == 1)) {
+#pragma unroll
+      for (int j = 0; j < MV; j++) {
+        const int m = (MB == 8 ? 4 * q : 0) + j;
+        rb[(wv * MB + m) * 16 + nl] = part[j];
+      }
+    }
     __syncthreads();
     for (int e = tid; e < M * 16; e += blockDim.x) {
       const int m = e >> 4, n = e & 15;
       float sum = 0.f;
-      for (int w2 = 0; w2 < W; w2++)
-#pragma unroll
-        for (int qq = 0; qq < 4; qq++)
-#pragma unroll
-          for (int v = 0; v < 4; v++) {
-            const int mp = 4 * qq + v;
-            if (mp % MB == m && mp / MB < NSLOT) sum += rb[(w2 * 64 + qq * 16 + n) * 4 + v];
-          }
+      for (int w2 = 0; w2 < W; w2++) sum += rb[(w2 * MB + m) * 16 + n];
       if (t * 16 + n < N) ((OS*)a.y)[(int64_t)m * N + t * 16 + n] = DT_<ODT>::from_f32(sum);
     }
   };
@@ -510,34 +535,46 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
   Regs r0, r1;
   const int step = gridDim.x;
   int t = blockIdx.x, rnd = 0;
-  issue(r0, t, 0);
 
   // ---- stage x + group sums (all threads) ----
-  {
-    const XS* xb = (const XS*)a.x;
-    const int cpr = K >> 3;
-    for (int e = tid; e < M * cpr; e += blockDim.x) {
-      const int m = e / cpr, c = e - m * cpr;
-      const int k = c * 8;
-      const u32x4 d = *reinterpret_cast<const u32x4*>(xb + (int64_t)m * K + k);
-      float sum = 0.f;
+  // The first two x loads of every thread go out before the first round's
+  // weight loads, so waiting for x does not wait for the weights (loads
+  // complete in issue order).
+  const XS* xb = (const XS*)a.x;
+  const int cpr = K >> 3;              // 8-element chunks per x row
+  const int items = M * cpr;           // multiple of 128 (K % 1024 == 0)
+  auto xload = [&](int e) -> u32x4 {
+    const int m = e / cpr, c = e - m * cpr;
+    return *reinterpret_cast<const u32x4*>(xb + (int64_t)m * K + c * 8);
+  };
+  auto stage = [&](int e, const u32x4 d) {
+    const int m = e / cpr, c = e - m * cpr;
+    float sum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; j++)
-        sum += DT_<XDT>::to_f32((uint16_t)(d[j] & 0xffffu)) + DT_<XDT>::to_f32((uint16_t)(d[j] >> 16));
-      u32x4 o;
-      o[0] = (d[0] & 0xffffu) | (d[2] << 16);
-      o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
-      o[2] = (d[1] & 0xffffu) | (d[3] << 16);
-      o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
-      *reinterpret_cast<u32x4*>(smem + ((size_t)m * K + k) * 2) = o;
+    for (int j = 0; j < 4; j++)
+      sum += DT_<XDT>::to_f32((uint16_t)(d[j] & 0xffffu)) + DT_<XDT>::to_f32((uint16_t)(d[j] >> 16));
+    u32x4 o;
+    o[0] = (d[0] & 0xffffu) | (d[2] << 16);
+    o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
+    o[2] = (d[1] & 0xffffu) | (d[3] << 16);
+    o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
+    *reinterpret_cast<u32x4*>(smem + ((size_t)m * K + c * 8) * 2) = o;
+    // GS/8 consecutive lanes hold one group
 #pragma unroll
-      for (int o2 = 1; o2 < GS / 8; o2 <<= 1) sum += __shfl_xor(sum, o2, 64);
-      if ((c & (GS / 8 - 1)) == 0) Xs[(c / (GS / 8)) * MB + m] = sum;
-    }
-    for (int e = tid; e < G * MB; e += blockDim.x)
-      if ((e % MB) >= M) Xs[e] = 0.f;
-    if (tid < 4) reinterpret_cast<u32x4*>(smem + zoff)[tid] = u32x4{0u, 0u, 0u, 0u};
-  }
+    for (int o2 = 1; o2 < GS / 8; o2 <<= 1) sum += __shfl_xor(sum, o2, 64);
+    if ((c & (GS / 8 - 1)) == 0) Xs[(c / (GS / 8)) * MB + m] = sum;
+  };
+  const int bd = blockDim.x;
+  u32x4 xd0 = {0u, 0u, 0u, 0u}, xd1 = {0u, 0u, 0u, 0u};
+  if (tid < items) xd0 = xload(tid);
+  if (tid + bd < items) xd1 = xload(tid + bd);
+  issue(r0, t, 0);
+  if (tid < items) stage(tid, xd0);
+  if (tid + bd < items) stage(tid + bd, xd1);
+  for (int e = tid + 2 * bd; e < items; e += bd) stage(e, xload(e));
+  for (int e = tid; e < G * MB; e += bd)
+    if ((e % MB) >= M) Xs[e] = 0.f;
+  if (tid < 4) reinterpret_cast<u32x4*>(smem + zoff)[tid] = u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
 
   // items (t, rnd) in order; buffers alternate, the next item's loads are
@@ -580,7 +617,7 @@ template <int XDT, int SDT, int MB, int GS, int S>
 hipError_t run_qmvp_s(const QArgs& a, int W, int R) {
   using C = PCfg<HQ_BITS, XDT, SDT, MB, GS, S>;
   const size_t G = (size_t)a.K / GS;
-  const size_t lds = (size_t)a.M * a.K * 2 + 64 + G * MB * 4 + (size_t)2 * W * 256 * 4;
+  const size_t lds = (size_t)a.M * a.K * 2 + 64 + G * MB * 4 + (size_t)2 * W * 16 * MB * 4;
   if (lds > 160 * 1024) return hipErrorNotSupported;
   PKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
