@@ -206,6 +206,219 @@ __global__ __launch_bounds__(256) void qmm_t_kernel(QKernM a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile GEMM for one product with 16-bit x and scales of the same type
+// (the prefill case): 256 x 256 output tile per 256-thread block, K-step 64.
+// The W tile is dequantized once per K-step into LDS as CT = round(s*q + b),
+// x is copied into LDS, both double-buffered: the global loads of step k+1
+// are in flight while the MFMAs of step k run. Each wave owns a 128 x 128
+// quarter of the tile as 8 x 8 fragments of v_mfma_f32_16x16x32 (fp32
+// accumulators). The MFMA computes the transposed product D[n][m] (A = W rows,
+// B = x rows) so every lane ends with 4 consecutive n of one m: 8-byte stores.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int GBM = 256, GBN = 256, GBK = 64;
+constexpr int GLD = GBK + 8;  // LDS row stride (elements): 144 B, conflict-free b128 reads
+
+struct GKern {
+  void* y;
+  const void* x;
+  const uint32_t* w;
+  const void* s;
+  const void* b;
+  int M, N, K;
+};
+
+template <int CT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (CT == DT_BF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    bf2 v;
+    v[0] = (__bf16)lo;
+    v[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 v;
+    v[0] = (_Float16)lo;
+    v[1] = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+template <int BITS, int CT, int GS>
+__global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
+  using T = Mma<CT>;
+  using ST = st_t<CT>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char gsm[];
+  uint16_t* As = reinterpret_cast<uint16_t*>(gsm);                    // [2][GBN][GLD]  (W)
+  uint16_t* Bs = As + 2 * GBN * GLD;                                  // [2][GBM][GLD]  (x)
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wn = wv >> 2, wm = wv & 3;  // wave owns n rows wn*128.., m rows wm*64..
+  const int M = a.M, N = a.N, K = a.K;
+  const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
+  const int64_t P = (int64_t)(K >> 5) * BITS;
+  const int64_t G = K / GS;
+  const ST* xg = (const ST*)a.x;
+  const ST* sg = (const ST*)a.s;
+  const ST* bg = (const ST*)a.b;
+
+  // x tile (256 x 64): thread copies rows xr + 64j (j < 4), 16-byte chunk xc.
+  // Rows past M read row M-1 (never stored), so every load is unconditional.
+  const int xr = tid >> 3, xc = tid & 7;
+  // W tile (256 x 64): thread dequantizes pack wp of row wr.
+  const int wr = tid >> 1, wp = tid & 1;
+  uint32_t xoff[4];  // element offsets into x (M*K < 2^31 is checked by the host)
+#pragma unroll
+  for (int j = 0; j < 4; j++) xoff[j] = (uint32_t)min(m0 + xr + 64 * j, M - 1) * (uint32_t)K + xc * 8;
+  const int wn_row = min(n0 + wr, N - 1);
+  const uint32_t woff = (uint32_t)((int64_t)wn_row * P) + wp * BITS;
+  const uint32_t goff = (uint32_t)((int64_t)wn_row * G);
+
+  struct WPre {
+    uint32_t wd[BITS];
+    float sv, bv;
+  };
+  u32x4 xv[4];
+  auto xload = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) xv[j] = *reinterpret_cast<const u32x4*>(xg + xoff[j] + k0);
+  };
+  auto xstore = [&](int buf) {
+    uint16_t* bs = Bs + buf * GBM * GLD;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      *reinterpret_cast<u32x4*>(bs + (xr + 64 * j) * GLD + xc * 8) = xv[j];
+  };
+  auto wload = [&](WPre& p, int k0) {
+    load_pack<BITS>(a.w + woff + (uint32_t)(k0 >> 5) * BITS, p.wd);
+    const uint32_t gi = goff + (uint32_t)((k0 + wp * 32) / GS);
+    p.sv = DT_<CT>::load(sg, gi);
+    p.bv = DT_<CT>::load(bg, gi);
+  };
+  // Quarter qq (8 elements) of this thread's pack, one 16-byte LDS store.
+  auto wchunk = [&](const WPre& p, int buf, int qq) {
+    uint16_t* dst = As + buf * GBN * GLD + wr * GLD + wp * 32 + qq * 8;
+    u32x4 h;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int i0 = qq * 8 + 2 * e;
+      h[e] = pack2<CT>(fmaf(p.sv, (float)pack_elem<BITS>(p.wd, i0), p.bv),
+                       fmaf(p.sv, (float)pack_elem<BITS>(p.wd, i0 + 1), p.bv));
+    }
+    *reinterpret_cast<u32x4*>(dst) = h;
+  };
+
+  floatx4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // MFMAs of one K-step on LDS buffer `buf`, with the dequantization of the
+  // next step's W (registers `wn_`) threaded between them into `buf ^ 1`.
+  auto step = [&](int buf, const WPre& wn_) {
+    const uint16_t* as = As + buf * GBN * GLD;
+    const uint16_t* bs = Bs + buf * GBM * GLD;
+#pragma unroll
+    for (int ks = 0; ks < GBK / 32; ks++) {
+      const int kofs = ks * 32 + (lane >> 4) * 8;
+      typename T::frag fb[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        fb[j] = __builtin_bit_cast(typename T::frag, *reinterpret_cast<const u32x4*>(
+                                                         bs + (wm * 64 + j * 16 + (lane & 15)) * GLD + kofs));
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const typename T::frag fa = __builtin_bit_cast(
+            typename T::frag,
+            *reinterpret_cast<const u32x4*>(as + (wn * 128 + i * 16 + (lane & 15)) * GLD + kofs));
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = T::mma(fa, fb[j], acc[i][j]);
+        if ((i & 3) == 0) wchunk(wn_, buf ^ 1, ks * 2 + (i >> 2));
+      }
+    }
+  };
+
+  // Pipeline: x one step ahead (plain copy), W two steps ahead (dequantized
+  // during the MFMAs of the step before it is used). Steps past the end
+  // reload step nk-1 (harmless).
+  const int nk = K / GBK;
+  WPre w0, w1;
+  xload(0);
+  wload(w0, 0);
+  wload(w1, min(1, nk - 1) * GBK);
+#pragma unroll
+  for (int c = 0; c < 4; c++) wchunk(w0, 0, c);
+  xstore(0);
+  __syncthreads();
+  // (One loop body; a manually unrolled ping-pong makes the register
+  // allocator spill the accumulators.)
+  for (int kt = 0; kt < nk; kt++) {
+    xload(min(kt + 1, nk - 1) * GBK);
+    wload(w0, min(kt + 2, nk - 1) * GBK);
+    step(kt & 1, w1);
+    xstore((kt & 1) ^ 1);
+    __syncthreads();
+    w1 = w0;
+  }
+
+  // epilogue: acc[i][j][v] = y[m][n], n = n0 + wn*128 + i*16 + 4*(lane>>4) + v,
+  // m = m0 + wm*64 + j*16 + (lane & 15)
+  ST* yg = (ST*)a.y;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int n = n0 + wn * 128 + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int m = m0 + wm * 64 + j * 16 + (lane & 15);
+      if (m >= M) continue;
+      if (n + 3 < N) {
+        u32x2 o;
+        o[0] = pack2<CT>(acc[i][j][0], acc[i][j][1]);
+        o[1] = pack2<CT>(acc[i][j][2], acc[i][j][3]);
+        *reinterpret_cast<u32x2*>(yg + (int64_t)m * N + n) = o;
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+          if (n + v < N) yg[(int64_t)m * N + n + v] = DT_<CT>::from_f32(acc[i][j][v]);
+      }
+    }
+  }
+}
+
+template <int CT, int GS>
+hipError_t run_qgemm(const QArgs& a) {
+  GKern k;
+  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
+  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
+  auto fn = qgemm_kernel<HQ_BITS, CT, GS>;
+  const size_t lds = (size_t)2 * (GBN + GBM) * GLD * 2;
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  dim3 grid((unsigned)((a.N + GBN - 1) / GBN), (unsigned)((a.M + GBM - 1) / GBM));
+  hipLaunchKernelGGL(fn, grid, dim3(512), lds, a.stream, k);
+  return hipGetLastError();
+}
+
+template <int CT>
+hipError_t run_qgemm_g(const QArgs& a) {
+  switch (a.group_size) {
+    case 32: return run_qgemm<CT, 32>(a);
+    case 64: return run_qgemm<CT, 64>(a);
+    default: return run_qgemm<CT, 128>(a);
+  }
+}
+
+}  // namespace
+
 template <int XDT, int SDT>
 static void run_qmm_t(const QArgs& a) {
   QKernM k;
@@ -223,6 +436,12 @@ static void run_qmm_t(const QArgs& a) {
 #define HQ_CAT(a, b) HQ_CAT_(a, b)
 
 hipError_t HQ_CAT(launch_qmm_t_b, HQ_BITS)(const QArgs& a) {
+  // One product with same-type 16-bit x and scales, K a multiple of the step:
+  // the large-tile GEMM. Everything else: the general batched kernel.
+  if (a.batch == 1 && !a.lhs && !a.rhs && a.xdt == a.sdt && a.xdt != DT_F32 &&
+      a.K % GBK == 0 && a.M >= 128) {
+    return a.xdt == DT_BF16 ? run_qgemm_g<DT_BF16>(a) : run_qgemm_g<DT_F16>(a);
+  }
   switch (a.xdt * 3 + a.sdt) {
     case DT_F32 * 3 + DT_F32: run_qmm_t<DT_F32, DT_F32>(a); break;
     case DT_F32 * 3 + DT_F16: run_qmm_t<DT_F32, DT_F16>(a); break;

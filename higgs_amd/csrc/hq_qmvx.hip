@@ -626,11 +626,24 @@ hipError_t run_qmvp_s(const QArgs& a, int W, int R) {
   k.off_pair = XMma<XDT>::OFFB;
   const int ntiles = (int)((a.N + 15) / 16);
   k.ntiles = ntiles;
-  const int per_cu = lds > 80 * 1024 ? 1 : 2;
+  auto fn = qmvp_kernel<HQ_BITS, XDT, SDT, MB, GS, S>;
+  // Blocks per CU: as many as LDS and registers keep resident at once (up to
+  // 4), so every block's tiles stream concurrently.
+  static int waves_per_simd = 0;
+  if (waves_per_simd == 0) {
+    hipFuncAttributes fa;
+    int vg = 128;
+    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)) == hipSuccess && fa.numRegs > 0)
+      vg = fa.numRegs;
+    waves_per_simd = vg <= 128 ? 4 : (vg <= 168 ? 3 : (vg <= 256 ? 2 : 1));
+  }
+  int per_cu = (int)((160 * 1024) / lds);
+  if (per_cu > 4) per_cu = 4;
+  if (per_cu > (4 * waves_per_simd) / W) per_cu = (4 * waves_per_simd) / W;
+  if (per_cu < 1) per_cu = 1;
   const int maxb = per_cu * device_cus();
   const int per = (ntiles + maxb - 1) / maxb;
   const int grid = (ntiles + per - 1) / per;
-  auto fn = qmvp_kernel<HQ_BITS, XDT, SDT, MB, GS, S>;
   static bool big_lds = false;
   if (lds > 64 * 1024 && !big_lds) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
