@@ -258,7 +258,18 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wn = wv >> 2, wm = wv & 3;  // wave owns n rows wn*128.., m rows wm*64..
   const int M = a.M, N = a.N, K = a.K;
-  const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
+  // XCD-aware tile order: consecutive block ids go to different XCDs (8 on
+  // MI355X), so tile t is given to block id (t % per) * 8 + t / per; each XCD
+  // then walks a contiguous, M-major range of tiles and keeps its x rows in
+  // its own L2 while the W tiles stream past.
+  const int ntn = (N + GBN - 1) / GBN;
+  const int ntiles = ntn * ((M + GBM - 1) / GBM);
+  int t = blockIdx.x;
+  if ((ntiles & 7) == 0) {
+    const int per = ntiles >> 3;
+    t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  }
+  const int n0 = (t % ntn) * GBN, m0 = (t / ntn) * GBM;
   const int64_t P = (int64_t)(K >> 5) * BITS;
   const int64_t G = K / GS;
   const ST* xg = (const ST*)a.x;
@@ -403,8 +414,8 @@ hipError_t run_qgemm(const QArgs& a) {
     if (e != hipSuccess) return e;
     attr = true;
   }
-  dim3 grid((unsigned)((a.N + GBN - 1) / GBN), (unsigned)((a.M + GBM - 1) / GBM));
-  hipLaunchKernelGGL(fn, grid, dim3(512), lds, a.stream, k);
+  const unsigned ntiles = (unsigned)(((a.N + GBN - 1) / GBN) * ((a.M + GBM - 1) / GBM));
+  hipLaunchKernelGGL(fn, dim3(ntiles), dim3(512), lds, a.stream, k);
   return hipGetLastError();
 }
 
