@@ -1,20 +1,34 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized-linear hot path on one MI355X.
 
-Workload: one Llama-3-8B decode step at batch B
-(default 1) = 32 layers x (q, k, v, o, gate, up, down) + lm_head, i.e. 225
-4-bit group-64 quantized GEMVs over 4.2 GB of distinct, HBM-resident weights
-(no cache reuse between steps: the working set is 16x the 256 MB MALL). The
-step is captured once in a HIP graph and replayed.
+Headline workload: one Llama-3-8B decode step at
+batch B (default 1) = 32 layers x (q, k, v, o, gate, up, down) + lm_head, i.e.
+225 4-bit group-64 quantized GEMVs over 4.2 GB of distinct weights resident in
+HBM (16x the 256 MB Infinity Cache, so every step streams from HBM). The step
+is captured once as a HIP graph and replayed; inputs are already in HBM when
+the timed region starts.
 
-Printed JSON line:
-  value        whole-step throughput, algorithmic bytes / step time (GB/s)
-  roofline     the qmv kernel: algorithmic bytes per launch / mean launch
-               duration (HIP events around each launch, on the launch stream)
-  qmm          configs[2] prefill GEMMs (M=2048), TFLOP/s and % of bf16 peak
-  qmv_batch    the same decode step at B = 1, 4, 8
-  cpu_baseline the oracle's MLX-CPU-style quantized_matmul on the host cores,
-               on a bounded sample (layer 0's seven projections at B)
+Printed JSON line (one, on stdout):
+  value         whole-step throughput: algorithmic bytes / step time (GB/s)
+  roofline      the qmv kernel (every launch of the step is one): algorithmic
+                bytes per launch / mean launch duration, the duration taken
+                from HIP events recorded on the replay stream around the timed
+                replays; peak = MI355X HBM3E 8 TB/s. `traffic` is the measured
+                HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+                WRITE_SIZE summary (profiles/), or null if absent.
+  qmv_shapes    per-projection mean launch time and GB/s (graph of the 32
+                distinct layer copies of that projection)
+  qmv_batch     the decode step at B = 1, 4, 8
+  qmm           configs[2]: M = 2048 prefill GEMMs, TFLOP/s and fraction of
+                the 2.5 PFLOP/s dense bf16 MFMA peak
+  moe           configs[4]: sorted gather_qmm (gate, down) at the MoE shapes
+  cpu_baseline  the CPU oracle's MLX-style quantized_matmul on the host cores,
+                on a bounded sample of the same workload (layer 0's seven
+                projections at B)
+
+Other modes (for profiling runs):
+  --mode copy   a plain device copy of --copy-mb MB (calibrates rocprofv3
+                FETCH_SIZE / WRITE_SIZE against known bytes)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
 """
@@ -23,6 +37,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -33,9 +48,10 @@ METRIC = "4-bit qmv GB/s (% HBM peak) + qmm TFLOPS (% MFMA peak), Llama-3-8B sha
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 BITS, GROUP = 4, 64
-HIDDEN, INTER, KV, VOCAB, LAYERS = 4096, 14336, 1024, 128256, 32
+HIDDEN, INTER, VOCAB, LAYERS = 4096, 14336, 128256, 32
 LAYER_SHAPES = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
                 ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmv_decode_llama3_8b_traffic.txt")
 
 
 def qmv_bytes(M, N, K, bits=BITS, g=GROUP):
@@ -65,124 +81,152 @@ class Model:
         self.lm_head = gen.torch_quantized(seed + 9999, VOCAB, HIDDEN, BITS, GROUP, dev)
         torch.cuda.synchronize()
 
-    def calls(self):
-        for l, ws in enumerate(self.layers):
+    def calls(self, only=None):
+        for ws in self.layers:
             for name, N, K in LAYER_SHAPES:
-                yield f"L{l}.{name}", name, ws[name], N, K
-        yield "lm_head", "lm_head", self.lm_head, VOCAB, HIDDEN
+                if only is None or only == name:
+                    yield name, ws[name], N, K
+        if only is None or only == "lm_head":
+            yield "lm_head", self.lm_head, VOCAB, HIDDEN
 
 
-class DecodeStep:
-    """Pre-bound C ABI calls for one decode step at batch B (no allocation)."""
+class Plan:
+    """Pre-bound C ABI calls (no allocation, no Python work per launch beyond
+    the call itself) for a list of projections at batch B."""
 
-    def __init__(self, model, B, dev):
+    def __init__(self, calls, B, dev):
         import torch
 
         from higgs_amd import _lib, gen
 
         self.lib = _lib.lib()
-        self.B = B
         self.xh = gen.torch_x(1, (B, HIDDEN), dev)
         self.xi = gen.torch_x(2, (B, INTER), dev)
         self.ys = {}
         self.plan = []
         self.bytes = 0
-        self.shape_of = []
-        for label, name, (w, s, b), N, K in model.calls():
+        for name, (w, s, b), N, K in calls:
             x = self.xi if K == INTER else self.xh
             if name not in self.ys:
                 self.ys[name] = torch.empty((B, N), dtype=torch.bfloat16, device=dev)
-            y = self.ys[name]
-            self.plan.append((y.data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(),
+            self.plan.append((self.ys[name].data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(),
                               b.data_ptr(), B, N, K))
             self.bytes += qmv_bytes(B, N, K)
-            self.shape_of.append((name, N, K))
 
-    def run(self, stream_ptr, events=None):
+    def run(self, stream_ptr):
         f = self.lib.hq_quantized_matmul
-        for i, (y, x, w, s, b, M, N, K) in enumerate(self.plan):
-            if events is not None:
-                events[i][0].record()
+        for (y, x, w, s, b, M, N, K) in self.plan:
             rc = f(y, x, w, s, b, M, N, K, 1, GROUP, BITS, 2, 2, stream_ptr)
-            if events is not None:
-                events[i][1].record()
             if rc:
                 from higgs_amd import _lib
                 raise _lib.HiggsQmmError(rc, _lib.last_error())
 
 
-def time_graph(step, steps, warmup, dev):
+def time_graph(run, steps, warmup, dev):
+    """Capture run(stream) once as a HIP graph; time `steps` replays with HIP
+    events recorded on the replay stream, synchronized on both sides.
+    Returns ms per replay."""
     import torch
 
-    stream = torch.cuda.current_stream(dev)
-    for _ in range(2):
-        step.run(stream.cuda_stream)
+    stream = torch.cuda.Stream(dev)
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            run(stream.cuda_stream)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream(dev)
-    cap.wait_stream(stream)
-    with torch.cuda.stream(cap):
-        with torch.cuda.graph(g, stream=cap):
-            step.run(cap.cuda_stream)
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            run(stream.cuda_stream)
     torch.cuda.synchronize()
-    for _ in range(warmup):
-        g.replay()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            g.replay()
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(steps):
-        g.replay()
-    t1.record()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(steps):
+            g.replay()
+        e1.record(stream)
     torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps, g
+    return e0.elapsed_time(e1) / steps
 
 
-def per_launch_durations(step, dev, reps=3):
-    """Mean duration (ms) of every launch of the step, timed with HIP events
-    recorded on the launch stream around each launch (eager, not graphed)."""
-    import torch
-
-    stream = torch.cuda.current_stream(dev)
-    n = len(step.plan)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(n)] for _ in range(reps)]
-    for r in range(reps):
-        step.run(stream.cuda_stream, evs[r])
-    torch.cuda.synchronize()
-    return [sum(evs[r][i][0].elapsed_time(evs[r][i][1]) for r in range(reps)) / reps
-            for i in range(n)]
+def read_traffic():
+    """HBM bytes per qmv launch measured by rocprofv3 (committed summary)."""
+    try:
+        txt = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
+    return float(m.group(1)) if m else None
 
 
-def bench_qmm(model, dev, reps=5):
-    """M=2048 prefill GEMMs on layer 0's gate and down weights."""
+def bench_shapes(model, B, dev, steps):
+    out = {}
+    for name, N, K in LAYER_SHAPES + [("lm_head", VOCAB, HIDDEN)]:
+        p = Plan(model.calls(only=name), B, dev)
+        ms = time_graph(p.run, steps, 2, dev)
+        n = len(p.plan)
+        out[name] = {"N": N, "K": K, "us_per_launch": round(ms * 1e3 / n, 3),
+                     "GB/s": round(p.bytes / (ms * 1e-3) / 1e9, 1)}
+    return out
+
+
+def bench_qmm(model, dev, steps):
+    """M=2048 prefill GEMMs over layer 0..3 gate and down weights."""
     import torch
 
     from higgs_amd import _lib, gen
 
     lib = _lib.lib()
     out = {}
-    stream = torch.cuda.current_stream(dev).cuda_stream
     for name, N, K in (("gate_up", INTER, HIDDEN), ("down", HIDDEN, INTER)):
-        w, s, b = model.layers[0]["gate" if name == "gate_up" else "down"]
+        ws = [model.layers[l]["gate" if name == "gate_up" else "down"] for l in range(4)]
         x = gen.torch_x(3, (2048, K), dev)
         y = torch.empty((2048, N), dtype=torch.bfloat16, device=dev)
-        args = (y.data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(), b.data_ptr(), 2048, N, K,
-                1, GROUP, BITS, 2, 2, stream)
-        for _ in range(2):
-            _lib.check(lib.hq_quantized_matmul(*args))
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            lib.hq_quantized_matmul(*args)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
+
+        def run(stream, ws=ws, x=x, y=y, N=N, K=K):
+            for (w, s, b) in ws:
+                _lib.check(lib.hq_quantized_matmul(y.data_ptr(), x.data_ptr(), w.data_ptr(),
+                                                   s.data_ptr(), b.data_ptr(), 2048, N, K, 1,
+                                                   GROUP, BITS, 2, 2, stream))
+        ms = time_graph(run, steps, 1, dev) / len(ws)
         tflops = 2.0 * 2048 * N * K / (ms * 1e-3) / 1e12
-        out[name] = {"M": 2048, "N": N, "K": K, "ms": round(ms, 4),
-                     "tflops": round(tflops, 2), "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+        out[name] = {"M": 2048, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                     "tflops": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+    return out
+
+
+def bench_moe(dev, steps):
+    """512 tokens, top-8 of 128 experts, hidden 2048, expert
+    intermediate 768, 4-bit g64; rows globally sorted by expert, sorted gather_qmm."""
+    import numpy as np
+    import torch
+
+    from higgs_amd import gen, ops
+
+    T, TK, E, H, I = 512, 8, 128, 2048, 768
+    idx = gen.topk_routing(3, T, E, TK).reshape(-1)
+    order = np.argsort(idx, kind="stable")
+    srt = torch.from_numpy(idx[order].astype(np.int32)).to(dev)
+    tok = torch.from_numpy((order // TK).astype(np.int64)).to(dev)
+    used = len(np.unique(idx))
+    out = {}
+    for name, N, K in (("gate", I, H), ("down", H, I)):
+        ws = [gen.torch_quantized(70 + c, N, K, BITS, GROUP, dev, lead=(E,)) for c in range(3)]
+        xs = gen.torch_x(71, (T, K), dev)[tok].reshape(-1, 1, K).contiguous()
+
+        def run(stream, ws=ws, xs=xs):
+            for (w, s, b) in ws:
+                ops.gather_qmm(xs, w, s, b, None, srt, True, GROUP, BITS, True)
+        ms = time_graph(run, steps, 1, dev) / len(ws)
+        byts = used * (N * K // 2 + 2 * N * (K // GROUP) * 2) + 2 * T * TK * (K + N)
+        out[name] = {"rows": T * TK, "experts": E, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                     "GB/s": round(byts / (ms * 1e-3) / 1e9, 1)}
+        del ws
+    torch.cuda.empty_cache()
     return out
 
 
@@ -190,6 +234,7 @@ def cpu_baseline(model, B, target_s):
     """Oracle quantized_matmul (MLX-CPU-style restatement, oracle/hq_oracle.c
     hqo_qmm_mlx) on the host, over layer 0's seven projections at batch B."""
     import numpy as np
+    import torch
 
     import oracle as O
     from higgs_amd import gen
@@ -198,7 +243,6 @@ def cpu_baseline(model, B, target_s):
     nbytes = 0
     for name, N, K in LAYER_SHAPES:
         w, s, b = model.layers[0][name]
-        import torch
         sample.append((w.cpu().numpy().view(np.uint32),
                        s.cpu().view(torch.int16).numpy().view(np.uint16),
                        b.cpu().view(torch.int16).numpy().view(np.uint16),
@@ -230,70 +274,85 @@ def cpu_baseline(model, B, target_s):
                       f"(float lanes, MLX CPU loop order)"}
 
 
+def mode_copy(dev, mb, steps):
+    import torch
+
+    n = mb * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"mode": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n,
+                      "ms": round(dt * 1e3, 4), "GB/s": round(8 * n / dt / 1e9, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=1)
-    ap.add_argument("--cpu-seconds", type=float, default=4.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0,
+                    help="target seconds per CPU thread-count leg")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip qmm and batch sweeps")
+    ap.add_argument("--no-extras", action="store_true", help="skip shapes, batch, qmm, moe")
+    ap.add_argument("--mode", default="decode", choices=("decode", "copy"))
+    ap.add_argument("--copy-mb", type=int, default=512)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
-              "multi-GPU path", file=sys.stderr)
+        print(f"bench.py measures one GPU (got --gpus {args.gpus}): this build's path is the "
+              "single-GPU quantized-linear kernel set; multi-GPU sharding is design-only",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
 
+    dev = torch.device("cuda:0")
+    if args.mode == "copy":
+        mode_copy(dev, args.copy_mb, args.steps)
+        return
+
     from higgs_amd import _lib
 
-    dev = torch.device("cuda:0")
     log(f"[bench] {_lib.version()} on {torch.cuda.get_device_name(0)}")
     model = Model(dev)
-    log("[bench] weights resident: %.2f GB" % (sum(
-        w.numel() * 4 + s.numel() * 2 + b.numel() * 2
-        for ws in model.layers for (w, s, b) in ws.values()) / 1e9))
+    step = Plan(model.calls(), args.batch, dev)
+    log(f"[bench] weights resident: {step.bytes / 1e9:.2f} GB algorithmic per step, "
+        f"{len(step.plan)} launches")
 
-    step = DecodeStep(model, args.batch, dev)
-    ms, _graph = time_graph(step, args.steps, args.warmup, dev)
+    ms = time_graph(step.run, args.steps, args.warmup, dev)
     value = step.bytes / (ms * 1e-3) / 1e9
-    log(f"[bench] decode step B={args.batch}: {ms:.4f} ms, {value:.1f} GB/s")
-
-    durs = per_launch_durations(step, dev)
-    tot_bytes = step.bytes
-    tot_ms = sum(durs)
-    achieved = tot_bytes / (tot_ms * 1e-3) / 1e9
-    per_shape = {}
-    for (name, N, K), d in zip(step.shape_of, durs):
-        e = per_shape.setdefault(name, {"N": N, "K": K, "launches": 0, "ms": 0.0})
-        e["launches"] += 1
-        e["ms"] += d
-    for name, e in per_shape.items():
-        e["us_per_launch"] = round(e["ms"] / e["launches"] * 1e3, 3)
-        e["GB/s"] = round(qmv_bytes(args.batch, e["N"], e["K"]) / (e["ms"] / e["launches"] * 1e-3)
-                          / 1e9, 1)
-        del e["ms"]
-    log(f"[bench] qmv kernel: {achieved:.1f} GB/s over {len(durs)} launches")
+    n_launch = len(step.plan)
+    mean_us = ms * 1e3 / n_launch
+    log(f"[bench] decode step B={args.batch}: {ms:.4f} ms, {value:.1f} GB/s, "
+        f"{mean_us:.3f} us per launch")
 
     extras = {}
     if not args.no_extras:
-        extras["qmm"] = bench_qmm(model, dev)
-        log(f"[bench] qmm: {extras['qmm']}")
+        extras["qmv_shapes"] = bench_shapes(model, args.batch, dev, max(3, args.steps // 4))
+        log(f"[bench] shapes: {extras['qmv_shapes']}")
         qb = {}
         for B in (1, 4, 8):
-            st = step if B == args.batch else DecodeStep(model, B, dev)
-            m, _ = time_graph(st, max(5, args.steps // 2), 2, dev)
+            st = step if B == args.batch else Plan(model.calls(), B, dev)
+            m = time_graph(st.run, max(5, args.steps // 2), 2, dev)
             qb[str(B)] = {"ms_per_step": round(m, 4), "GB/s": round(st.bytes / (m * 1e-3) / 1e9, 1)}
         extras["qmv_batch"] = qb
-        log(f"[bench] qmv batch sweep: {qb}")
+        log(f"[bench] batch sweep: {qb}")
+        extras["qmm"] = bench_qmm(model, dev, max(3, args.steps // 4))
+        log(f"[bench] qmm: {extras['qmm']}")
+        extras["moe"] = bench_moe(dev, max(3, args.steps // 4))
+        log(f"[bench] moe: {extras['moe']}")
 
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(model, args.batch, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu}")
 
+    traffic = read_traffic()
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -305,19 +364,21 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "u4 x bf16",
         "data": "synthetic",
-        "config": {"workload": f"Llama-3-8B decode step, 32 layers x (q,k,v,o,gate,up,down) + "
-                               f"lm_head, B={args.batch}, 4-bit g64 qmv (configs[1])",
+        "config": {"workload": f"Llama-3-8B decode step (configs[1]): 32 layers x (q,k,v,o,"
+                               f"gate,up,down) + lm_head at B={args.batch}, 4-bit g64 "
+                               f"quantized_matmul, one HIP graph",
                    "bits": BITS, "group_size": GROUP, "batch": args.batch,
-                   "weights_GB": round(tot_bytes / 1e9, 3), "launches_per_step": len(step.plan),
+                   "algorithmic_GB_per_step": round(step.bytes / 1e9, 4),
+                   "launches_per_step": n_launch,
                    "compute": "u4 weights x bf16 activations, fp32 accumulate, bf16 out"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": f"qmv (4-bit g64, bf16, M={args.batch})",
-                     "bytes_per_launch": round(tot_bytes / len(durs)),
-                     "mean_launch_us": round(tot_ms / len(durs) * 1e3, 3)},
-        "qmv_shapes": per_shape,
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
+                     "traffic": round(traffic) if traffic else None,
+                     "kernel": "qmvp_kernel (matrix-core decode GEMV), every launch of the step",
+                     "bytes_per_launch": round(step.bytes / n_launch),
+                     "mean_launch_us": round(mean_us, 3)},
         "cpu_baseline": cpu,
     }
     line.update(extras)

@@ -63,6 +63,7 @@ hipError_t dispatch_q(int bits, const hq::QArgs& a, int which) {
     if (which == 0) return hq::launch_qmv_t_b##B(a);   \
     if (which == 1) return hq::launch_qmm_t_b##B(a);   \
     if (which == 3) return hq::launch_qmvx_t_b##B(a);  \
+    if (which == 4) return hq::launch_gqmm_t_b##B(a);  \
     return hq::launch_qmv_n_b##B(a);
   switch (bits) {
     HQ_Q_CASE(2)
@@ -92,6 +93,15 @@ int run_q(const char* tag, int bits, hq::QArgs& a, int transpose) {
   // 0: VALU GEMV (fp32 x), 3: matrix-core GEMV (16-bit x), 1: GEMM, 2: transpose=false.
   int which = !transpose ? 2 : (a.M <= hq::kQmvMaxM ? 0 : 1);
   if (which == 0 && a.xdt != HQ_DTYPE_FLOAT32) which = 3;
+  // Sorted expert indices: the grouped kernel streams each expert's weights
+  // once for all of its rows. It declines shapes it does not take.
+  if (transpose && a.sorted && a.batch > 1) {
+    hipError_t e = dispatch_q(bits, a, 4);
+    if (e == hipSuccess) return HQ_OK;
+    if (e != hipErrorNotSupported)
+      return fail(HQ_ERR_HIP, "[%s] kernel launch failed: %s", tag, hipGetErrorString(e));
+    (void)hipGetLastError();
+  }
   if (which == 1 && a.M > hq::kQmmMaxM)
     return fail(HQ_ERR_UNSUPPORTED, "[%s] M=%lld exceeds the GEMM grid limit (%lld rows).", tag,
                 (long long)a.M, (long long)hq::kQmmMaxM);

@@ -50,6 +50,7 @@ struct DeqArgs {
   hipError_t launch_dequant_b##B(const DeqArgs& a);      \
   hipError_t launch_qmv_t_b##B(const QArgs& a);          \
   hipError_t launch_qmvx_t_b##B(const QArgs& a);         \
+  hipError_t launch_gqmm_t_b##B(const QArgs& a);         \
   hipError_t launch_qmm_t_b##B(const QArgs& a);          \
   hipError_t launch_qmv_n_b##B(const QArgs& a);
 

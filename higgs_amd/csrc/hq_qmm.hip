@@ -247,6 +247,33 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   }
 }
 
+// Eight consecutive elements (pack quarter qq) of a 32-element pack,
+// dequantized to CT as round(s * q + b), as four packed pairs. For 4 bits the
+// even and odd nibbles of the word are masked to bytes once, so each element
+// costs one v_cvt_f32_ubyteN, one FMA and half a v_cvt_pk.
+template <int BITS, int CT>
+__device__ __forceinline__ u32x4 deq8(const uint32_t (&wd)[BITS], int qq, float s, float b) {
+  u32x4 h;
+  if constexpr (BITS == 4) {
+    const uint32_t w = wd[qq];
+    const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float q0 = (float)((ev >> (8 * e)) & 0xffu);  // element 2e
+      const float q1 = (float)((od >> (8 * e)) & 0xffu);  // element 2e + 1
+      h[e] = pack2<CT>(fmaf(s, q0, b), fmaf(s, q1, b));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int i0 = qq * 8 + 2 * e;
+      h[e] = pack2<CT>(fmaf(s, (float)pack_elem<BITS>(wd, i0), b),
+                       fmaf(s, (float)pack_elem<BITS>(wd, i0 + 1), b));
+    }
+  }
+  return h;
+}
+
 template <int BITS, int CT, int GS>
 __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   using T = Mma<CT>;
@@ -312,14 +339,7 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   // Quarter qq (8 elements) of this thread's pack, one 16-byte LDS store.
   auto wchunk = [&](const WPre& p, int buf, int qq) {
     uint16_t* dst = As + buf * GBN * GLD + wr * GLD + wp * 32 + qq * 8;
-    u32x4 h;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int i0 = qq * 8 + 2 * e;
-      h[e] = pack2<CT>(fmaf(p.sv, (float)pack_elem<BITS>(p.wd, i0), p.bv),
-                       fmaf(p.sv, (float)pack_elem<BITS>(p.wd, i0 + 1), p.bv));
-    }
-    *reinterpret_cast<u32x4*>(dst) = h;
+    *reinterpret_cast<u32x4*>(dst) = deq8<BITS, CT>(p.wd, qq, p.sv, p.bv);
   };
 
   floatx4 acc[8][4];
@@ -428,7 +448,242 @@ hipError_t run_qgemm_g(const QArgs& a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped GEMM for gather_qmm with sorted expert indices (the MoE global-sort
+// path: SwitchMlpWeights::forward_gather_global_sort, crates/higgs-models/src/
+// qwen3_next.rs:1731-1809, calls gather_qmm with sorted_indices = true).
+// Block (nt, e) owns W rows nt*128.. of expert e. It finds the run of batch
+// elements whose rhs index is e (two rounds of a 64-wide search over the
+// sorted indices), then multiplies every row of that run, 64 rows at a time,
+// by its W tile -- each expert's weights stream from HBM once per 64 rows.
+// The extra block row e == w_batch fills the rows of out-of-range indices
+// (sorted to the end) with NaN. Same LDS-dequant MFMA pipeline as the
+// large-tile GEMM, at a 128 x 64 tile with 4 waves (2 blocks per CU).
+// ---------------------------------------------------------------------------
+constexpr int QBN = 128, QBM = 64;
+constexpr int kGD = 4;  // register prefetch depth (K-steps) of the grouped kernel
+
+struct GQKern {
+  void* y;
+  const void* x;
+  const uint32_t* w;
+  const void* s;
+  const void* b;
+  const uint32_t* lhs;
+  const uint32_t* rhs;
+  int64_t batch, x_rep, x_batch, w_batch;
+  int M, N, K;
+};
+
+// First index i in [0, n) with v[i] >= key (n if none), for non-decreasing v.
+// Wave-uniform result; two or three rounds of 64 probes for n <= 2^18.
+__device__ __forceinline__ int64_t wave_lower_bound(const uint32_t* v, int64_t n, uint32_t key) {
+  const int lane = threadIdx.x & 63;
+  int64_t lo = 0, hi = n;  // v[j] < key for j < lo; answer in [lo, hi]
+  while (lo < hi) {
+    const int64_t step = (hi - lo + 63) / 64;
+    const int64_t p = lo + (int64_t)lane * step;
+    const bool less = p < hi && v[p] < key;
+    const int c = __popcll(__ballot(less));  // probes below key form a prefix
+    if (c == 0) return lo;                  // v[lo] >= key
+    const int64_t nlo = lo + (int64_t)(c - 1) * step + 1;
+    const int64_t nhi = min(hi, lo + (int64_t)c * step);
+    if (step == 1) return nhi;
+    lo = nlo;
+    hi = nhi;
+  }
+  return lo;
+}
+
+template <int BITS, int CT, int GS>
+__global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
+  using T = Mma<CT>;
+  using ST = st_t<CT>;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][QBN * GLD];  // W (dequantized)
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][QBM * GLD];  // x rows
+  __shared__ int64_t run[2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int M = a.M, N = a.N, K = a.K;
+  const int n0 = blockIdx.x * QBN;
+  const int64_t e = blockIdx.y;  // expert, or w_batch for the out-of-range tail
+  if (wv == 0) {
+    const int64_t s0 = wave_lower_bound(a.rhs, a.batch, (uint32_t)e);
+    const int64_t s1 = e < a.w_batch ? wave_lower_bound(a.rhs, a.batch, (uint32_t)(e + 1)) : a.batch;
+    if (lane == 0) { run[0] = s0; run[1] = s1; }
+  }
+  __syncthreads();
+  const int64_t r_begin = run[0] * M, r_end = run[1] * M;  // flattened (element, m) rows
+  if (r_begin >= r_end) return;
+  ST* yg = (ST*)a.y;
+  if (e >= a.w_batch) {
+    const uint16_t nan16 = CT == DT_BF16 ? 0x7fc0u : 0x7e00u;
+    for (int64_t r = r_begin; r < r_end; r++)
+      for (int n = n0 + tid; n < min(n0 + QBN, N); n += 256) yg[r * N + n] = nan16;
+    return;
+  }
+
+  const int64_t P = (int64_t)(K >> 5) * BITS;
+  const int64_t G = K / GS;
+  const ST* xg = (const ST*)a.x;
+  const ST* sg = (const ST*)a.s + e * (int64_t)N * G;
+  const ST* bg = (const ST*)a.b + e * (int64_t)N * G;
+  const uint32_t* wg = a.w + e * (int64_t)N * P;
+  const int wn = wv;  // wave owns W rows wn*32.. (2 fragments), all 64 x rows
+
+  // x tile (64 x 64): thread copies chunks xc and xc + 4 of row xr.
+  const int xr = tid >> 2, xc = tid & 3;
+  // W tile (128 x 64): thread dequantizes pack wp of row wr.
+  const int wr = tid >> 1, wp = tid & 1;
+  const int n_w = min(n0 + wr, N - 1);
+  const uint32_t* wrow = wg + (int64_t)n_w * P + wp * BITS;
+  const ST* srow = sg + (int64_t)n_w * G;
+  const ST* brow = bg + (int64_t)n_w * G;
+
+  struct WPre {
+    uint32_t wd[BITS];
+    float sv, bv;
+  };
+  auto wload = [&](WPre& p, int k0) {
+    load_pack<BITS>(wrow + (int64_t)(k0 >> 5) * BITS, p.wd);
+    const int gi = (k0 + wp * 32) / GS;
+    p.sv = DT_<CT>::load(srow, gi);
+    p.bv = DT_<CT>::load(brow, gi);
+  };
+  auto wstore = [&](const WPre& p, int buf) {
+    uint16_t* dst = As[buf] + wr * GLD + wp * 32;
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) *reinterpret_cast<u32x4*>(dst + qq * 8) = deq8<BITS, CT>(p.wd, qq, p.sv, p.bv);
+  };
+
+  for (int64_t r0 = r_begin; r0 < r_end; r0 += QBM) {
+    // this thread's x row: flattened row r -> batch element r / M, row r % M
+    const int64_t r = min(r0 + xr, r_end - 1);
+    const int64_t bi = r / M;
+    const int64_t xi = a.lhs ? (int64_t)a.lhs[bi] : bi / a.x_rep;
+    const ST* xrow = xg + (min(xi, a.x_batch - 1) * M + (r - bi * M)) * (int64_t)K + xc * 8;
+
+    floatx4 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // Register ring of kGD steps: the loads of step kt + kGD are issued at
+    // step kt and land in LDS at step kt + kGD - 1, so kGD - 1 steps of
+    // compute cover their latency. The ring index is a compile-time constant
+    // inside the unrolled group, so no register copies force early waits.
+    const int nk = K / GBK;
+    WPre wr_[kGD];
+    u32x4 xr_[kGD][2];
+    auto xload_to = [&](u32x4 (&d)[2], int k0) {
+      d[0] = *reinterpret_cast<const u32x4*>(xrow + k0);
+      d[1] = *reinterpret_cast<const u32x4*>(xrow + k0 + 32);
+    };
+    auto xstore_from = [&](const u32x4 (&d)[2], int buf) {
+      *reinterpret_cast<u32x4*>(Bs[buf] + xr * GLD + xc * 8) = d[0];
+      *reinterpret_cast<u32x4*>(Bs[buf] + xr * GLD + xc * 8 + 32) = d[1];
+    };
+#pragma unroll
+    for (int d = 0; d < kGD; d++) {
+      xload_to(xr_[d], min(d, nk - 1) * GBK);
+      wload(wr_[d], min(d, nk - 1) * GBK);
+    }
+    wstore(wr_[0], 0);
+    xstore_from(xr_[0], 0);
+    __syncthreads();
+    for (int kt0 = 0; kt0 < nk; kt0 += kGD) {
+#pragma unroll
+      for (int d = 0; d < kGD; d++) {
+        const int kt = kt0 + d;
+        if (kt < nk) {
+          const int buf = d & 1;  // kGD is even, so kt & 1 == d & 1
+#pragma unroll
+          for (int ks = 0; ks < GBK / 32; ks++) {
+            const int kofs = ks * 32 + (lane >> 4) * 8;
+            typename T::frag fb[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+              fb[j] = __builtin_bit_cast(typename T::frag, *reinterpret_cast<const u32x4*>(
+                                                               Bs[buf] + (j * 16 + (lane & 15)) * GLD + kofs));
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+              const typename T::frag fa = __builtin_bit_cast(
+                  typename T::frag,
+                  *reinterpret_cast<const u32x4*>(As[buf] + (wn * 32 + i * 16 + (lane & 15)) * GLD + kofs));
+#pragma unroll
+              for (int j = 0; j < 4; j++) acc[i][j] = T::mma(fa, fb[j], acc[i][j]);
+            }
+          }
+          // step kt + 1 (ring slot d + 1) into the other buffer; refill slot d
+          // with step kt + kGD (past the end: reload the last step, unused)
+          wstore(wr_[(d + 1) % kGD], buf ^ 1);
+          xstore_from(xr_[(d + 1) % kGD], buf ^ 1);
+          xload_to(xr_[d], min(kt + kGD, nk - 1) * GBK);
+          wload(wr_[d], min(kt + kGD, nk - 1) * GBK);
+          __syncthreads();
+        }
+      }
+    }
+
+    // epilogue: acc[i][j][v] = y[row m][n], n = n0 + wn*32 + i*16 + 4*(lane>>4) + v
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int n = n0 + wn * 32 + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int64_t rr = r0 + j * 16 + (lane & 15);
+        if (rr >= r_end) continue;
+        const int64_t rb = rr / M;
+        if ((a.lhs ? (int64_t)a.lhs[rb] : rb / a.x_rep) >= a.x_batch) {  // out-of-range x index
+#pragma unroll
+          for (int v = 0; v < 4; v++)
+            if (n + v < N) yg[rr * N + n + v] = CT == DT_BF16 ? (uint16_t)0x7fc0u : (uint16_t)0x7e00u;
+          continue;
+        }
+        if (n + 3 < N) {
+          u32x2 o;
+          o[0] = pack2<CT>(acc[i][j][0], acc[i][j][1]);
+          o[1] = pack2<CT>(acc[i][j][2], acc[i][j][3]);
+          *reinterpret_cast<u32x2*>(yg + rr * N + n) = o;
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; v++)
+            if (n + v < N) yg[rr * N + n + v] = DT_<CT>::from_f32(acc[i][j][v]);
+        }
+      }
+    }
+  }
+}
+
+template <int CT, int GS>
+hipError_t run_gqmm(const QArgs& a) {
+  GQKern k;
+  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b; k.lhs = a.lhs; k.rhs = a.rhs;
+  k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
+  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
+  dim3 grid((unsigned)((a.N + QBN - 1) / QBN), (unsigned)(a.w_batch + 1));
+  hipLaunchKernelGGL((gqmm_kernel<HQ_BITS, CT, GS>), grid, dim3(256), 0, a.stream, k);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+#define HQ_CAT_(a, b) a##b
+#define HQ_CAT(a, b) HQ_CAT_(a, b)
+
+// Sorted-index gather_qmm through the grouped kernel, or hipErrorNotSupported
+// (dtype mix, K not a multiple of 64, too many experts for the grid).
+hipError_t HQ_CAT(launch_gqmm_t_b, HQ_BITS)(const QArgs& a) {
+  if (a.xdt != a.sdt || a.xdt == DT_F32 || a.K % GBK != 0 || a.w_batch + 1 > 65535 || !a.rhs)
+    return hipErrorNotSupported;
+  const bool bf = a.xdt == DT_BF16;
+  switch (a.group_size) {
+    case 32: return bf ? run_gqmm<DT_BF16, 32>(a) : run_gqmm<DT_F16, 32>(a);
+    case 64: return bf ? run_gqmm<DT_BF16, 64>(a) : run_gqmm<DT_F16, 64>(a);
+    default: return bf ? run_gqmm<DT_BF16, 128>(a) : run_gqmm<DT_F16, 128>(a);
+  }
+}
 
 template <int XDT, int SDT>
 static void run_qmm_t(const QArgs& a) {
@@ -442,9 +697,6 @@ static void run_qmm_t(const QArgs& a) {
             (unsigned)(a.batch < 65535 ? a.batch : 65535));
   qmm_t_kernel<HQ_BITS, XDT, SDT><<<grid, 256, 0, a.stream>>>(k);
 }
-
-#define HQ_CAT_(a, b) a##b
-#define HQ_CAT(a, b) HQ_CAT_(a, b)
 
 hipError_t HQ_CAT(launch_qmm_t_b, HQ_BITS)(const QArgs& a) {
   // One product with same-type 16-bit x and scales, K a multiple of the step:

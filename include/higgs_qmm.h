@@ -104,8 +104,11 @@ int hq_quantized_matmul(void* y, const void* x, const uint32_t* w,
  * element repeated batch/x_batch times (batch % x_batch must be 0). Other
  * broadcasts pass explicit lhs_indices.
  * sorted_indices != 0 promises rhs_indices is non-decreasing (the global
- * expert sort); it selects the grouped kernel that reads each expert's
- * weights once per run of equal indices. Results do not depend on it.
+ * expert sort, qwen3_next.rs:1748-1761); with transpose != 0 and same-type
+ * 16-bit x and scales it selects the grouped kernel, which streams each
+ * expert's weights once for all rows of that expert. As with MLX's sorted
+ * path, the promise is relied on: unsorted indices with sorted_indices != 0
+ * give unspecified results. sorted_indices == 0 accepts any order.
  * Indices out of range (xi >= x_batch or wi >= w_batch) never cause an
  * out-of-bounds read: their output rows are filled with NaN.
  */

@@ -1,0 +1,122 @@
+"""gather_qmm on the MoE global-sort path (Qwen3-30B-A3B
+style, 128 experts, top-8 of 512 tokens, hidden 2048, expert intermediate 768,
+4-bit g64), through the C ABI via the torch facade, against the CPU oracle.
+
+The reference's own checks are relational (crates/higgs-models/src/
+qwen3_next.rs:4344-4398 gather == per-expert quantized_matmul;
+4431-4530 global-sort == unsorted path); these tests assert the same
+relations plus absolute parity with the fp64 oracle on sampled rows
+(max|y-r| / max|r| <= 1e-2 for bf16 output).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import idx_dev, rel_err, to_host_bits
+from higgs_amd import gen, ops
+
+pytestmark = pytest.mark.gpu
+
+TOKENS, TOPK, E, HID, INTER, G, BITS = 512, 8, 128, 2048, 768, 64, 4
+
+
+def _host(t):
+    return to_host_bits(t)
+
+
+def _routing(seed=3):
+    idx = gen.topk_routing(seed, TOKENS, E, TOPK)           # [512, 8]
+    order, inv, srt, tok = O.gather_sort(idx, TOPK)          # qwen3_next.rs:1748-1761
+    return idx, order, inv, srt, tok
+
+
+def _oracle_rows(xs, W, S, B, idx_rows, rows, N, K):
+    """fp64 reference for the sampled rows: y[i] = x_sorted[i] . deq(W[idx[i]])^T."""
+    w = W.cpu().numpy().view(np.uint32)
+    s = S.cpu().view(torch.int16).numpy().view(np.uint16)
+    b = B.cpu().view(torch.int16).numpy().view(np.uint16)
+    x = xs.cpu().view(torch.int16).numpy().view(np.uint16).reshape(-1, K)
+    out = np.empty((len(rows), N))
+    for j, r in enumerate(rows):
+        e = int(idx_rows[r])
+        out[j] = O.qmm_f64(x[r:r + 1], O.BF16, w[e], s[e], b[e], O.BF16, G, BITS)[0]
+    return out
+
+
+@pytest.mark.parametrize("which", ["gate", "down"])
+def test_c4_sorted_gather_matches_oracle(dev, which):
+    N, K = (INTER, HID) if which == "gate" else (HID, INTER)
+    idx, order, inv, srt, tok = _routing()
+    W, S, B = gen.torch_quantized(40, N, K, BITS, G, dev, lead=(E,))
+    x = gen.torch_x(41, (TOKENS, K), dev)
+    xs = x[torch.from_numpy(tok.astype(np.int64)).to(dev)].reshape(-1, 1, K)
+    y = ops.gather_qmm(xs, W, S, B, None, idx_dev(srt, dev), True, G, BITS, True)
+    assert tuple(y.shape) == (TOKENS * TOPK, 1, N)
+    rng = np.random.default_rng(5)
+    # every expert's first and last row plus random rows
+    firsts = np.searchsorted(srt, np.arange(E))
+    lasts = np.searchsorted(srt, np.arange(E), side="right") - 1
+    rows = np.unique(np.concatenate([firsts[firsts < len(srt)], lasts[lasts >= 0],
+                                     rng.integers(0, len(srt), 64)]))
+    ref = _oracle_rows(xs, W, S, B, srt, rows, N, K)
+    got = y.float().cpu().numpy().reshape(-1, N)[rows].astype(np.float64)
+    assert rel_err(got, ref) <= 1e-2
+
+
+def test_c4_sorted_equals_unsorted_and_unsort_roundtrip(dev):
+    # qwen3_next.rs:4431-4530: the global-sort path equals the plain path.
+    idx, order, inv, srt, tok = _routing(7)
+    W, S, B = gen.torch_quantized(42, INTER, HID, BITS, G, dev, lead=(E,))
+    x = gen.torch_x(43, (TOKENS, HID), dev)
+    # plain path (forward_gather, qwen3_next.rs:1660-1720): x [L,1,1,D] vs idx [L,k]
+    base = ops.gather_qmm(x.reshape(TOKENS, 1, 1, HID), W, S, B, None,
+                          idx_dev(idx, dev), True, G, BITS, False)      # [512, 8, 1, 768]
+    xs = x[torch.from_numpy(tok.astype(np.int64)).to(dev)].reshape(-1, 1, HID)
+    ys = ops.gather_qmm(xs, W, S, B, None, idx_dev(srt, dev), True, G, BITS, True)
+    unsorted = ys.reshape(-1, INTER)[torch.from_numpy(inv.astype(np.int64)).to(dev)]
+    a = unsorted.float()
+    b = base.reshape(-1, INTER).float()
+    assert (a - b).abs().max().item() <= 1e-2 * b.abs().max().item()
+
+
+def test_sorted_gather_via_lhs_indices_equals_materialized(dev):
+    # Fusing the token gather into gather_qmm (lhs_indices = token of each
+    # sorted row) gives exactly the materialized x_sorted result.
+    idx, order, inv, srt, tok = _routing(9)
+    W, S, B = gen.torch_quantized(44, INTER, HID, BITS, G, dev, lead=(E,))
+    x = gen.torch_x(45, (TOKENS, HID), dev)
+    xs = x[torch.from_numpy(tok.astype(np.int64)).to(dev)].reshape(-1, 1, HID)
+    y1 = ops.gather_qmm(xs, W, S, B, None, idx_dev(srt, dev), True, G, BITS, True)
+    y2 = ops.gather_qmm(x.reshape(TOKENS, 1, HID), W, S, B, idx_dev(tok, dev),
+                        idx_dev(srt, dev), True, G, BITS, True)
+    assert torch.equal(y1, y2)
+
+
+def test_sorted_gather_out_of_range_rows_are_nan(dev):
+    N, K, Ex = 128, 256, 4
+    W, S, B = gen.torch_quantized(46, N, K, BITS, G, dev, lead=(Ex,))
+    x = gen.torch_x(47, (10, 1, K), dev)
+    rhs = np.array([0, 0, 1, 2, 2, 2, 3, 9, 9, 11], np.uint32)   # last 3 out of range
+    y = ops.gather_qmm(x, W, S, B, None, idx_dev(rhs, dev), True, G, BITS, True)
+    assert torch.isnan(y[7:]).all() and not torch.isnan(y[:7]).any()
+    ref = O.gather_qmm_f64(_host(x), O.BF16, W.cpu().numpy().view(np.uint32),
+                           _host(S), _host(B), O.BF16, np.arange(7, dtype=np.uint32), rhs[:7],
+                           1, N, K, G, BITS, x_batch=10)
+    assert rel_err(y[:7].float().cpu().numpy().astype(np.float64), ref) <= 1e-2
+    lhs = np.array([0, 1, 2, 3, 4, 5, 77, 7, 8, 9], np.uint32)    # x index 77 out of range
+    y2 = ops.gather_qmm(x, W, S, B, idx_dev(lhs, dev), idx_dev(rhs, dev), True, G, BITS, True)
+    assert torch.isnan(y2[6]).all() and not torch.isnan(y2[:6]).any()
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_sorted_gather_small_matches_per_expert(dev, M):
+    # qwen3_next.rs:4344-4398 on the sorted path, with M rows per element
+    N, K, Ex = 192, 512, 6
+    W, S, B = gen.torch_quantized(48, N, K, BITS, G, dev, lead=(Ex,))
+    rhs = np.array([0, 1, 1, 1, 4, 4, 5], np.uint32)
+    x = gen.torch_x(49, (len(rhs), M, K), dev)
+    y = ops.gather_qmm(x, W, S, B, None, idx_dev(rhs, dev), True, G, BITS, True)
+    for i, e in enumerate(rhs):
+        one = ops.quantized_matmul(x[i], W[e], S[e], B[e], True, G, BITS)
+        assert (y[i].float() - one.float()).abs().max().item() <= 1e-2 * one.float().abs().max().item()

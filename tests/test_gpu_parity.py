@@ -217,21 +217,28 @@ def test_gather_out_of_range_gives_nan(dev):
     assert not torch.isnan(y[1]).any()
 
 
-def test_sorted_equals_unsorted_and_global_sort_roundtrip(dev):
-    # qwen3_next.rs:4431-4530 (global sort == baseline), 1731-1809 (sort/unsort)
+@pytest.mark.parametrize("dt", [O.F32, O.BF16])
+def test_sorted_equals_unsorted_and_global_sort_roundtrip(dev, dt):
+    # qwen3_next.rs:4431-4530 (global sort == baseline), 1731-1809 (sort/unsort).
+    # The reference asserts max |diff| < 1e-5 in float32; in bfloat16 the two
+    # paths run different kernels and may differ by an output rounding.
     E, D, I, L, k = 8, 64, 64, 16, 3
-    wg, sg, bg = _experts(50, E, I, D, 4, 64)
-    x = x_of(51, (1, L, D), O.BF16)
+    wg, sg, bg = _experts(50, E, I, D, 4, 64, dt)
+    x = x_of(51, (1, L, D), dt)
     idx = (np.arange(L * k) % E).astype(np.uint32).reshape(1, L, k)
-    Wd, Sd, Bd = words_dev(wg, dev), to_dev(sg, O.BF16, dev), to_dev(bg, O.BF16, dev)
-    xd = to_dev(x, O.BF16, dev)
+    Wd, Sd, Bd = words_dev(wg, dev), to_dev(sg, dt, dev), to_dev(bg, dt, dev)
+    xd = to_dev(x, dt, dev)
     base = ops.gather_qmm(xd.reshape(1, L, 1, 1, D), Wd, Sd, Bd, None, idx_dev(idx, dev), True,
                           64, 4, False).reshape(L * k, I)
     order, inv, srt, tok = O.gather_sort(idx, k)
     xs = xd.reshape(L, 1, D)[torch.from_numpy(tok.astype(np.int64)).to(dev)]
     ys = ops.gather_qmm(xs, Wd, Sd, Bd, None, idx_dev(srt, dev), True, 64, 4, True).reshape(-1, I)
     unsorted = ys[torch.from_numpy(inv.astype(np.int64)).to(dev)]
-    assert torch.equal(unsorted, base)
+    diff = (unsorted.float() - base.float()).abs().max().item()
+    if dt == O.F32:
+        assert diff < 1e-5
+    else:
+        assert diff <= 1e-2 * base.float().abs().max().item()
 
 
 @pytest.mark.parametrize("xdt,sdt", [(O.F32, O.F32), (O.F16, O.F16), (O.BF16, O.F16)])
