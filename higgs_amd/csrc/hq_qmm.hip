@@ -219,7 +219,8 @@ __global__ __launch_bounds__(256) void qmm_t_kernel(QKernM a) {
 namespace {
 
 constexpr int GBM = 256, GBN = 256, GBK = 64;
-constexpr int GLD = GBK + 8;  // LDS row stride (elements): 144 B, conflict-free b128 reads
+constexpr int kRD = 3;  // register prefetch depth (K-steps) of the large-tile GEMM
+constexpr int GLD = GBK + 16;  // LDS row stride (elements): 160 B (fewest bank conflicts measured)
 
 struct GKern {
   void* y;
@@ -319,17 +320,6 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
     uint32_t wd[BITS];
     float sv, bv;
   };
-  u32x4 xv[4];
-  auto xload = [&](int k0) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) xv[j] = *reinterpret_cast<const u32x4*>(xg + xoff[j] + k0);
-  };
-  auto xstore = [&](int buf) {
-    uint16_t* bs = Bs + buf * GBM * GLD;
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      *reinterpret_cast<u32x4*>(bs + (xr + 64 * j) * GLD + xc * 8) = xv[j];
-  };
   auto wload = [&](WPre& p, int k0) {
     load_pack<BITS>(a.w + woff + (uint32_t)(k0 >> 5) * BITS, p.wd);
     const uint32_t gi = goff + (uint32_t)((k0 + wp * 32) / GS);
@@ -373,27 +363,47 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
     }
   };
 
-  // Pipeline: x one step ahead (plain copy), W two steps ahead (dequantized
-  // during the MFMAs of the step before it is used). Steps past the end
-  // reload step nk-1 (harmless).
+  // Register ring of kRD K-steps for x and W, indexed by compile-time slots
+  // inside an unrolled group of 2*kRD steps: the loads of step kt + kRD are
+  // issued at step kt and reach LDS at step kt + kRD - 1, so kRD - 1 steps of
+  // MFMAs cover their latency. (Rotating registers by copies instead would
+  // make every copy wait for the loads just issued.)
   const int nk = K / GBK;
-  WPre w0, w1;
-  xload(0);
-  wload(w0, 0);
-  wload(w1, min(1, nk - 1) * GBK);
+  WPre wr_[kRD];
+  u32x4 xr_[kRD][4];
+  auto xload_to = [&](u32x4 (&d)[4], int k0) {
 #pragma unroll
-  for (int c = 0; c < 4; c++) wchunk(w0, 0, c);
-  xstore(0);
+    for (int j = 0; j < 4; j++) d[j] = *reinterpret_cast<const u32x4*>(xg + xoff[j] + k0);
+  };
+  auto xstore_from = [&](const u32x4 (&d)[4], int buf) {
+    uint16_t* bs = Bs + buf * GBM * GLD;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      *reinterpret_cast<u32x4*>(bs + (xr + 64 * j) * GLD + xc * 8) = d[j];
+  };
+#pragma unroll
+  for (int d = 0; d < kRD; d++) {
+    xload_to(xr_[d], min(d, nk - 1) * GBK);
+    wload(wr_[d], min(d, nk - 1) * GBK);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; c++) wchunk(wr_[0], 0, c);
+  xstore_from(xr_[0], 0);
   __syncthreads();
-  // (One loop body; a manually unrolled ping-pong makes the register
-  // allocator spill the accumulators.)
-  for (int kt = 0; kt < nk; kt++) {
-    xload(min(kt + 1, nk - 1) * GBK);
-    wload(w0, min(kt + 2, nk - 1) * GBK);
-    step(kt & 1, w1);
-    xstore((kt & 1) ^ 1);
-    __syncthreads();
-    w1 = w0;
+  for (int kt0 = 0; kt0 < nk; kt0 += 2 * kRD) {
+#pragma unroll
+    for (int dd = 0; dd < 2 * kRD; dd++) {
+      const int kt = kt0 + dd;
+      if (kt < nk) {
+        const int d = dd % kRD, buf = dd & 1;
+        step(buf, wr_[(d + 1) % kRD]);
+        xstore_from(xr_[(d + 1) % kRD], buf ^ 1);
+        // past the end: reload the last step (unused)
+        xload_to(xr_[d], min(kt + kRD, nk - 1) * GBK);
+        wload(wr_[d], min(kt + kRD, nk - 1) * GBK);
+        __syncthreads();
+      }
+    }
   }
 
   // epilogue: acc[i][j][v] = y[m][n], n = n0 + wn*128 + i*16 + 4*(lane>>4) + v,

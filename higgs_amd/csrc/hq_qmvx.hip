@@ -665,14 +665,21 @@ hipError_t run_qmvp(const QArgs& a) {
     if (a.K % 1024 != 0) return hipErrorNotSupported;
     const int nseg = (int)(a.K / 128);
     const int ntiles = (int)((a.N + 15) / 16);
-    // S = 8 segments per round; W waves such that W * 8 divides nseg, as many
-    // as fit 8 (more waves per tile when there are few tiles).
-    int W = 0;
-    const int wmax = 8;
-    for (int c = wmax; c >= 1; c--)
-      if ((nseg / 8) % c == 0) { W = c; break; }
-    if (W == 0) return hipErrorNotSupported;
-    return run_qmvp_s<XDT, SDT, MB, GS, 8>(a, W, nseg / (8 * W));
+    // S = 8 segments per round and W <= 8 waves with W * 8 dividing nseg.
+    // When that leaves fewer than 8 waves per tile and tiles are few (small
+    // N), rounds of S = 4 give each tile up to twice the waves.
+    auto pick = [&](int S) {
+      for (int c = 8; c >= 1; c--)
+        if ((nseg / S) % c == 0) return c;
+      return 0;
+    };
+    const int W8 = pick(8);
+    if (W8 < 8 && ntiles <= 512) {
+      const int W4 = pick(4);
+      if (W4 > W8) return run_qmvp_s<XDT, SDT, MB, GS, 4>(a, W4, nseg / (4 * W4));
+    }
+    if (W8 == 0) return hipErrorNotSupported;
+    return run_qmvp_s<XDT, SDT, MB, GS, 8>(a, W8, nseg / (8 * W8));
   }
 }
 
