@@ -33,6 +33,13 @@ SIGNATURES = {
     "hq_dequantize": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp]),
     "hq_embedding_dequantize": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int,
                                        _int, _vp]),
+    "hq_quantized_matmul_swiglu": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                          _i64, _int, _int, _int, _int, _vp]),
+    "hq_gather_qmm_swiglu": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                    _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _vp]),
+    "hq_swiglu": (_int, [_vp, _vp, _vp, _i64, _int, _vp]),
+    "hq_moe_sort": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "hq_moe_combine": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
 }
 
 

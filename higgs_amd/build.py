@@ -25,7 +25,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 BITS = (2, 3, 4, 5, 6, 8)
 PER_BITS = ("hq_dequant.hip", "hq_qmv.hip", "hq_qmvx.hip", "hq_qmm.hip")
-ONCE = ("hq_capi.hip",)
+ONCE = ("hq_capi.hip", "hq_moe.hip")
 
 # -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 (see
 # DESIGN.md, hardware notes). Denormals are kept so fp16/fp32 dequantize

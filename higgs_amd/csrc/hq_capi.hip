@@ -14,6 +14,7 @@
 
 #include "../../include/higgs_qmm.h"
 #include "hq_kernels.hpp"
+#include "hq_moe.hpp"
 
 namespace {
 
@@ -239,6 +240,186 @@ int hq_embedding_dequantize(void* out, const uint32_t* w, const void* scales, co
     return fail(HQ_ERR_INVALID_ARGUMENT, "[embedding_dequantize] indices must not be NULL.");
   return deq_common("embedding_dequantize", out, w, scales, biases, indices, n, rows, K, group_size,
                     bits, s_dtype, stream);
+}
+
+int hq_quantized_matmul_swiglu(void* h, const void* x, const uint32_t* w_gate,
+                               const void* s_gate, const void* b_gate, const uint32_t* w_up,
+                               const void* s_up, const void* b_up, int64_t M, int64_t N, int64_t K,
+                               int group_size, int bits, int x_dtype, int s_dtype, void* stream) {
+  const char* tag = "quantized_matmul_swiglu";
+  int rc = check_common(tag, group_size, bits, x_dtype, s_dtype);
+  if (rc) return rc;
+  if (M < 0 || N < 0 || K <= 0 || M > kMaxDim || N > kMaxDim || K > kMaxDim)
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] Invalid sizes M=%lld N=%lld K=%lld.", tag,
+                (long long)M, (long long)N, (long long)K);
+  if (K % group_size)
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] The last dimension of the quantized matrix (%lld) must be divisible by the "
+                "group size %d (transpose=1).",
+                tag, (long long)K, group_size);
+  if (M == 0 || N == 0) return HQ_OK;
+  if (!h || !x || !w_gate || !s_gate || !b_gate || !w_up || !s_up || !b_up)
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] NULL buffer pointer.", tag);
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(h))
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] x, w_gate, w_up and h must be 16-byte aligned.",
+                tag);
+  if (x_dtype != s_dtype || x_dtype == HQ_DTYPE_FLOAT32)
+    return fail(HQ_ERR_UNSUPPORTED,
+                "[%s] The fused kernel takes x and scales of one 16-bit dtype (got %d, %d).", tag,
+                x_dtype, s_dtype);
+  const bool gemm = M > 127;
+  if (gemm ? (K % 64 != 0) : (K % 1024 != 0))
+    return fail(HQ_ERR_UNSUPPORTED,
+                "[%s] K=%lld: the fused kernel needs K %% %d == 0 at M=%lld.", tag, (long long)K,
+                gemm ? 64 : 1024, (long long)M);
+  hq::QArgs a{};
+  a.y = h; a.x = x; a.w = w_gate; a.s = s_gate; a.b = b_gate;
+  a.w2 = w_up; a.s2 = s_up; a.b2 = b_up;
+  a.lhs = nullptr; a.rhs = nullptr;
+  a.batch = 1; a.x_rep = 1; a.x_batch = 1; a.w_batch = 1;
+  a.N = N; a.K = K;
+  a.group_size = group_size; a.xdt = x_dtype; a.sdt = s_dtype; a.sorted = 0;
+  a.stream = (hipStream_t)stream;
+  hipError_t e = hipSuccess;
+  if (gemm) {
+    a.M = M;
+    e = dispatch_q(bits, a, 1);
+  } else {
+    // GEMV kernel, up to kQmvMaxM rows of x per launch
+    const size_t xb = x_dtype == HQ_DTYPE_FLOAT32 ? 4 : 2;
+    for (int64_t m0 = 0; m0 < M && e == hipSuccess; m0 += hq::kQmvMaxM) {
+      a.M = M - m0 < hq::kQmvMaxM ? M - m0 : hq::kQmvMaxM;
+      a.x = static_cast<const char*>(x) + (size_t)(m0 * K) * xb;
+      a.y = static_cast<char*>(h) + (size_t)(m0 * N) * xb;
+      e = dispatch_q(bits, a, 3);
+    }
+  }
+  if (e == hipErrorNotSupported) {
+    (void)hipGetLastError();
+    return fail(HQ_ERR_UNSUPPORTED, "[%s] shape M=%lld N=%lld K=%lld not taken by the fused kernel.",
+                tag, (long long)M, (long long)N, (long long)K);
+  }
+  if (e != hipSuccess)
+    return fail(HQ_ERR_HIP, "[%s] kernel launch failed: %s", tag, hipGetErrorString(e));
+  return HQ_OK;
+}
+
+int hq_gather_qmm_swiglu(void* h, const void* x, const uint32_t* w_gate, const void* s_gate,
+                         const void* b_gate, const uint32_t* w_up, const void* s_up,
+                         const void* b_up, const uint32_t* lhs_indices,
+                         const uint32_t* rhs_indices, int64_t batch, int64_t x_batch,
+                         int64_t w_batch, int64_t M, int64_t N, int64_t K, int group_size,
+                         int bits, int x_dtype, int s_dtype, void* stream) {
+  const char* tag = "gather_qmm_swiglu";
+  int rc = check_common(tag, group_size, bits, x_dtype, s_dtype);
+  if (rc) return rc;
+  if (batch < 0 || x_batch <= 0 || w_batch <= 0 || M < 0 || N < 0 || K <= 0 || M > kMaxDim ||
+      N > kMaxDim || K > kMaxDim || batch > ((int64_t)1 << 40))
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] Invalid sizes batch=%lld x_batch=%lld w_batch=%lld M=%lld N=%lld K=%lld.",
+                tag, (long long)batch, (long long)x_batch, (long long)w_batch, (long long)M,
+                (long long)N, (long long)K);
+  if (K % group_size)
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] The last dimension of the quantized matrix (%lld) must be divisible by the "
+                "group size %d (transpose=1).",
+                tag, (long long)K, group_size);
+  if (!lhs_indices && batch % x_batch)
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] Without lhs_indices the batch (%lld) must be a multiple of x's batch (%lld).",
+                tag, (long long)batch, (long long)x_batch);
+  if (batch == 0 || M == 0 || N == 0) return HQ_OK;
+  if (!rhs_indices)
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] rhs_indices must not be NULL.", tag);
+  if (!h || !x || !w_gate || !s_gate || !b_gate || !w_up || !s_up || !b_up)
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] NULL buffer pointer.", tag);
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(h))
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] x, w_gate, w_up and h must be 16-byte aligned.",
+                tag);
+  hq::QArgs a{};
+  a.y = h; a.x = x; a.w = w_gate; a.s = s_gate; a.b = b_gate;
+  a.w2 = w_up; a.s2 = s_up; a.b2 = b_up;
+  a.lhs = lhs_indices; a.rhs = rhs_indices;
+  a.batch = batch; a.x_rep = lhs_indices ? 1 : batch / x_batch;
+  a.x_batch = x_batch; a.w_batch = w_batch;
+  a.M = M; a.N = N; a.K = K;
+  a.group_size = group_size; a.xdt = x_dtype; a.sdt = s_dtype; a.sorted = 1;
+  a.stream = (hipStream_t)stream;
+  hipError_t e = dispatch_q(bits, a, 4);
+  if (e == hipErrorNotSupported) {
+    (void)hipGetLastError();
+    return fail(HQ_ERR_UNSUPPORTED,
+                "[%s] the fused grouped kernel needs x and scales of one 16-bit dtype, K %% 64 "
+                "== 0 and w_batch < 65535 (got dtypes %d, %d, K=%lld, w_batch=%lld).",
+                tag, x_dtype, s_dtype, (long long)K, (long long)w_batch);
+  }
+  if (e != hipSuccess)
+    return fail(HQ_ERR_HIP, "[%s] kernel launch failed: %s", tag, hipGetErrorString(e));
+  return HQ_OK;
+}
+
+int hq_swiglu(void* out, const void* gate, const void* up, int64_t n, int dtype, void* stream) {
+  const char* tag = "swiglu";
+  if (!dtype_ok(dtype))
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] Only real floating types are supported but the dtype code is %d.", tag, dtype);
+  if (n < 0 || n > ((int64_t)1 << 40))
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] Invalid size n=%lld.", tag, (long long)n);
+  if (n == 0) return HQ_OK;
+  if (!out || !gate || !up) return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] NULL buffer pointer.", tag);
+  hipError_t e = hq::launch_swiglu(gate, up, out, n, dtype, (hipStream_t)stream);
+  if (e != hipSuccess)
+    return fail(HQ_ERR_HIP, "[%s] kernel launch failed: %s", tag, hipGetErrorString(e));
+  return HQ_OK;
+}
+
+int hq_moe_sort(uint32_t* order, uint32_t* inv_order, uint32_t* idx_sorted, uint32_t* token_idx,
+                const uint32_t* idx, int64_t n, int64_t top_k, int64_t num_experts, void* stream) {
+  const char* tag = "moe_sort";
+  if (n < 0 || n >= ((int64_t)1 << 31) || top_k <= 0 || num_experts <= 0 ||
+      num_experts > hq::kSortMaxExperts)
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] Invalid sizes n=%lld top_k=%lld num_experts=%lld (num_experts <= %lld, "
+                "n < 2^31).",
+                tag, (long long)n, (long long)top_k, (long long)num_experts,
+                (long long)hq::kSortMaxExperts);
+  if (n == 0) return HQ_OK;
+  if (!idx) return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] idx must not be NULL.", tag);
+  hq::SortArgs a{};
+  a.idx = idx; a.n = n; a.top_k = top_k; a.E = num_experts;
+  a.order = order; a.inv_order = inv_order; a.idx_sorted = idx_sorted; a.token_idx = token_idx;
+  a.stream = (hipStream_t)stream;
+  hipError_t e = hq::launch_moe_sort(a);
+  if (e != hipSuccess)
+    return fail(HQ_ERR_HIP, "[%s] kernel launch failed: %s", tag, hipGetErrorString(e));
+  return HQ_OK;
+}
+
+int hq_moe_combine(void* out, const void* y, const uint32_t* inv_order, const void* scores,
+                   int64_t tokens, int64_t top_k, int64_t D, int dtype, int score_dtype,
+                   void* stream) {
+  const char* tag = "moe_combine";
+  if (!dtype_ok(dtype) || !dtype_ok(score_dtype))
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] Only real floating types are supported but the dtype codes are %d, %d.", tag,
+                dtype, score_dtype);
+  if (tokens < 0 || top_k <= 0 || D <= 0 || tokens > kMaxDim || top_k > 4096 || D > kMaxDim ||
+      tokens * top_k >= ((int64_t)1 << 32))
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] Invalid sizes tokens=%lld top_k=%lld D=%lld.", tag,
+                (long long)tokens, (long long)top_k, (long long)D);
+  if (tokens == 0) return HQ_OK;
+  if (!out || !y || !inv_order || !scores)
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] NULL buffer pointer.", tag);
+  if (!aligned16(y) || !aligned16(out))
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] y and out must be 16-byte aligned.", tag);
+  hq::CombineArgs a{};
+  a.out = out; a.y = y; a.inv_order = inv_order; a.scores = scores;
+  a.tokens = tokens; a.top_k = top_k; a.D = D; a.dt = dtype; a.sdt = score_dtype;
+  a.stream = (hipStream_t)stream;
+  hipError_t e = hq::launch_moe_combine(a);
+  if (e != hipSuccess)
+    return fail(HQ_ERR_HIP, "[%s] kernel launch failed: %s", tag, hipGetErrorString(e));
+  return HQ_OK;
 }
 
 }  // extern "C"

@@ -71,6 +71,14 @@ template <> struct DT_<DT_F16> {
 
 template <int DT> using st_t = typename DT_<DT>::storage;
 
+// SwiGLU of one (gate, up) pair: gate * sigmoid(gate) * up
+// (crates/higgs-models/src/qwen3_next.rs:340-342). Callers pass gate and up
+// already rounded to the output dtype, as the reference materialises both
+// projections before the elementwise op, and round the result once.
+__device__ __forceinline__ float swiglu_f32(float g, float u) {
+  return g / (1.f + __expf(-g)) * u;
+}
+
 // Load 8 consecutive elements (16 B for 16-bit types, 32 B for float32) and
 // widen to float. `p` must be 16-B aligned for 16-bit types.
 template <int DT>

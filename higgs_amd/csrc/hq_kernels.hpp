@@ -29,6 +29,12 @@ struct QArgs {
   int group_size;
   int xdt, sdt;         // hq dtype codes
   int sorted;           // rhs is non-decreasing
+  // SwiGLU fusion: when w2 is set, (w, s, b) is the gate projection and
+  // (w2, s2, b2) the up projection, both N x K, and y = swiglu(x.Wg^T, x.Wu^T)
+  // (N columns). Null for a plain product.
+  const uint32_t* w2;
+  const void* s2;
+  const void* b2;
   hipStream_t stream;
 };
 

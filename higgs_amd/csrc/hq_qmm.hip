@@ -229,6 +229,9 @@ struct GKern {
   const void* s;
   const void* b;
   int M, N, K;
+  const uint32_t* w2;  // SwiGLU up projection (gate is w/s/b), N rows
+  const void* s2;
+  const void* b2;
 };
 
 template <int CT>
@@ -275,7 +278,11 @@ __device__ __forceinline__ u32x4 deq8(const uint32_t (&wd)[BITS], int qq, float 
   return h;
 }
 
-template <int BITS, int CT, int GS>
+// SWI: the 256 W rows of a tile are 128 output columns of the gate and the
+// same 128 columns of the up projection, arranged so that a wave's fragments
+// i < 4 are gate rows and i + 4 the matching up rows; the epilogue writes
+// swiglu(gate, up) for 128 columns from registers.
+template <int BITS, int CT, int GS, bool SWI>
 __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   using T = Mma<CT>;
   using ST = st_t<CT>;
@@ -290,38 +297,43 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   // MI355X), so tile t is given to block id (t % per) * 8 + t / per; each XCD
   // then walks a contiguous, M-major range of tiles and keeps its x rows in
   // its own L2 while the W tiles stream past.
-  const int ntn = (N + GBN - 1) / GBN;
+  constexpr int ONT = SWI ? GBN / 2 : GBN;  // output columns per tile
+  const int ntn = (N + ONT - 1) / ONT;
   const int ntiles = ntn * ((M + GBM - 1) / GBM);
   int t = blockIdx.x;
   if ((ntiles & 7) == 0) {
     const int per = ntiles >> 3;
     t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
   }
-  const int n0 = (t % ntn) * GBN, m0 = (t / ntn) * GBM;
+  const int n0 = (t % ntn) * ONT, m0 = (t / ntn) * GBM;
   const int64_t P = (int64_t)(K >> 5) * BITS;
   const int64_t G = K / GS;
   const ST* xg = (const ST*)a.x;
-  const ST* sg = (const ST*)a.s;
-  const ST* bg = (const ST*)a.b;
 
   // x tile (256 x 64): thread copies rows xr + 64j (j < 4), 16-byte chunk xc.
   // Rows past M read row M-1 (never stored), so every load is unconditional.
   const int xr = tid >> 3, xc = tid & 7;
   // W tile (256 x 64): thread dequantizes pack wp of row wr.
   const int wr = tid >> 1, wp = tid & 1;
-  uint32_t xoff[4];  // element offsets into x (M*K < 2^31 is checked by the host)
+  uint32_t xoff[4];  // element offsets into x (the launcher checks M*K < 2^31)
 #pragma unroll
   for (int j = 0; j < 4; j++) xoff[j] = (uint32_t)min(m0 + xr + 64 * j, M - 1) * (uint32_t)K + xc * 8;
-  const int wn_row = min(n0 + wr, N - 1);
+  // SWI: tile row wr is column n0 + (wr / 128) * 64 + wr % 64 of the gate
+  // (wr % 128 < 64) or of the up projection.
+  const bool w_up = SWI && (wr & 64);
+  const int wn_row = min(SWI ? n0 + (wr >> 7) * 64 + (wr & 63) : n0 + wr, N - 1);
   const uint32_t woff = (uint32_t)((int64_t)wn_row * P) + wp * BITS;
   const uint32_t goff = (uint32_t)((int64_t)wn_row * G);
+  const uint32_t* wg = w_up ? a.w2 : a.w;
+  const ST* sg = (const ST*)(w_up ? a.s2 : a.s);
+  const ST* bg = (const ST*)(w_up ? a.b2 : a.b);
 
   struct WPre {
     uint32_t wd[BITS];
     float sv, bv;
   };
   auto wload = [&](WPre& p, int k0) {
-    load_pack<BITS>(a.w + woff + (uint32_t)(k0 >> 5) * BITS, p.wd);
+    load_pack<BITS>(wg + woff + (uint32_t)(k0 >> 5) * BITS, p.wd);
     const uint32_t gi = goff + (uint32_t)((k0 + wp * 32) / GS);
     p.sv = DT_<CT>::load(sg, gi);
     p.bv = DT_<CT>::load(bg, gi);
@@ -409,6 +421,33 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   // epilogue: acc[i][j][v] = y[m][n], n = n0 + wn*128 + i*16 + 4*(lane>>4) + v,
   // m = m0 + wm*64 + j*16 + (lane & 15)
   ST* yg = (ST*)a.y;
+  if constexpr (SWI) {
+    // acc[i] gate and acc[i + 4] up of column n0 + wn*64 + i*16 + 4*(lane>>4) + v
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int n = n0 + wn * 64 + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int m = m0 + wm * 64 + j * 16 + (lane & 15);
+        if (m >= M) continue;
+        float h[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+          h[v] = swiglu_f32(DT_<CT>::round(acc[i][j][v]), DT_<CT>::round(acc[i + 4][j][v]));
+        if (n + 3 < N) {
+          u32x2 o;
+          o[0] = pack2<CT>(h[0], h[1]);
+          o[1] = pack2<CT>(h[2], h[3]);
+          *reinterpret_cast<u32x2*>(yg + (int64_t)m * N + n) = o;
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; v++)
+            if (n + v < N) yg[(int64_t)m * N + n + v] = DT_<CT>::from_f32(h[v]);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 8; i++) {
     const int n = n0 + wn * 128 + i * 16 + 4 * (lane >> 4);
@@ -430,12 +469,13 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   }
 }
 
-template <int CT, int GS>
+template <int CT, int GS, bool SWI>
 hipError_t run_qgemm(const QArgs& a) {
   GKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
-  auto fn = qgemm_kernel<HQ_BITS, CT, GS>;
+  k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
+  auto fn = qgemm_kernel<HQ_BITS, CT, GS, SWI>;
   const size_t lds = (size_t)2 * (GBN + GBM) * GLD * 2;
   static bool attr = false;
   if (!attr) {
@@ -444,17 +484,18 @@ hipError_t run_qgemm(const QArgs& a) {
     if (e != hipSuccess) return e;
     attr = true;
   }
-  const unsigned ntiles = (unsigned)(((a.N + GBN - 1) / GBN) * ((a.M + GBM - 1) / GBM));
+  const int ont = SWI ? GBN / 2 : GBN;
+  const unsigned ntiles = (unsigned)(((a.N + ont - 1) / ont) * ((a.M + GBM - 1) / GBM));
   hipLaunchKernelGGL(fn, dim3(ntiles), dim3(512), lds, a.stream, k);
   return hipGetLastError();
 }
 
-template <int CT>
+template <int CT, bool SWI = false>
 hipError_t run_qgemm_g(const QArgs& a) {
   switch (a.group_size) {
-    case 32: return run_qgemm<CT, 32>(a);
-    case 64: return run_qgemm<CT, 64>(a);
-    default: return run_qgemm<CT, 128>(a);
+    case 32: return run_qgemm<CT, 32, SWI>(a);
+    case 64: return run_qgemm<CT, 64, SWI>(a);
+    default: return run_qgemm<CT, 128, SWI>(a);
   }
 }
 
@@ -483,6 +524,9 @@ struct GQKern {
   const uint32_t* rhs;
   int64_t batch, x_rep, x_batch, w_batch;
   int M, N, K;
+  const uint32_t* w2;  // SwiGLU up projection (gate is w/s/b), [w_batch, N, P]
+  const void* s2;
+  const void* b2;
 };
 
 // First index i in [0, n) with v[i] >= key (n if none), for non-decreasing v.
@@ -505,7 +549,11 @@ __device__ __forceinline__ int64_t wave_lower_bound(const uint32_t* v, int64_t n
   return lo;
 }
 
-template <int BITS, int CT, int GS>
+// SWI: a tile's 128 W rows are 64 output columns of the gate and the same
+// columns of the up projection; wave wn's fragment 0 holds gate columns
+// n0 + wn*16 .. + 15 and fragment 1 the matching up columns, so the epilogue
+// writes swiglu(gate, up) from registers.
+template <int BITS, int CT, int GS, bool SWI>
 __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
   using T = Mma<CT>;
   using ST = st_t<CT>;
@@ -515,7 +563,8 @@ __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int M = a.M, N = a.N, K = a.K;
-  const int n0 = blockIdx.x * QBN;
+  constexpr int ONT = SWI ? QBN / 2 : QBN;  // output columns per tile
+  const int n0 = blockIdx.x * ONT;
   const int64_t e = blockIdx.y;  // expert, or w_batch for the out-of-range tail
   if (wv == 0) {
     const int64_t s0 = wave_lower_bound(a.rhs, a.batch, (uint32_t)e);
@@ -529,23 +578,26 @@ __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
   if (e >= a.w_batch) {
     const uint16_t nan16 = CT == DT_BF16 ? 0x7fc0u : 0x7e00u;
     for (int64_t r = r_begin; r < r_end; r++)
-      for (int n = n0 + tid; n < min(n0 + QBN, N); n += 256) yg[r * N + n] = nan16;
+      for (int n = n0 + tid; n < min(n0 + ONT, N); n += 256) yg[r * N + n] = nan16;
     return;
   }
 
   const int64_t P = (int64_t)(K >> 5) * BITS;
   const int64_t G = K / GS;
   const ST* xg = (const ST*)a.x;
-  const ST* sg = (const ST*)a.s + e * (int64_t)N * G;
-  const ST* bg = (const ST*)a.b + e * (int64_t)N * G;
-  const uint32_t* wg = a.w + e * (int64_t)N * P;
   const int wn = wv;  // wave owns W rows wn*32.. (2 fragments), all 64 x rows
 
   // x tile (64 x 64): thread copies chunks xc and xc + 4 of row xr.
   const int xr = tid >> 2, xc = tid & 3;
-  // W tile (128 x 64): thread dequantizes pack wp of row wr.
+  // W tile (128 x 64): thread dequantizes pack wp of row wr. SWI: row wr is
+  // column n0 + (wr / 32) * 16 + wr % 16 of the gate (bit 4 of wr clear) or
+  // of the up projection.
   const int wr = tid >> 1, wp = tid & 1;
-  const int n_w = min(n0 + wr, N - 1);
+  const bool w_up = SWI && (wr & 16);
+  const ST* sg = (const ST*)(w_up ? a.s2 : a.s) + e * (int64_t)N * G;
+  const ST* bg = (const ST*)(w_up ? a.b2 : a.b) + e * (int64_t)N * G;
+  const uint32_t* wg = (w_up ? a.w2 : a.w) + e * (int64_t)N * P;
+  const int n_w = min(SWI ? n0 + (wr >> 5) * 16 + (wr & 15) : n0 + wr, N - 1);
   const uint32_t* wrow = wg + (int64_t)n_w * P + wp * BITS;
   const ST* srow = sg + (int64_t)n_w * G;
   const ST* brow = bg + (int64_t)n_w * G;
@@ -637,9 +689,17 @@ __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
     }
 
     // epilogue: acc[i][j][v] = y[row m][n], n = n0 + wn*32 + i*16 + 4*(lane>>4) + v
+    // (SWI: acc[0] gate and acc[1] up of column n0 + wn*16 + 4*(lane>>4) + v)
+    if constexpr (SWI) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int n = n0 + wn * 32 + i * 16 + 4 * (lane >> 4);
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+          acc[0][j][v] = swiglu_f32(DT_<CT>::round(acc[0][j][v]), DT_<CT>::round(acc[1][j][v]));
+    }
+#pragma unroll
+    for (int i = 0; i < (SWI ? 1 : 2); i++) {
+      const int n = n0 + wn * (SWI ? 16 : 32) + i * 16 + 4 * (lane >> 4);
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const int64_t rr = r0 + j * 16 + (lane & 15);
@@ -666,15 +726,27 @@ __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
   }
 }
 
-template <int CT, int GS>
+template <int CT, int GS, bool SWI>
 hipError_t run_gqmm(const QArgs& a) {
   GQKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b; k.lhs = a.lhs; k.rhs = a.rhs;
   k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
-  dim3 grid((unsigned)((a.N + QBN - 1) / QBN), (unsigned)(a.w_batch + 1));
-  hipLaunchKernelGGL((gqmm_kernel<HQ_BITS, CT, GS>), grid, dim3(256), 0, a.stream, k);
+  k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
+  const int ont = SWI ? QBN / 2 : QBN;
+  dim3 grid((unsigned)((a.N + ont - 1) / ont), (unsigned)(a.w_batch + 1));
+  hipLaunchKernelGGL((gqmm_kernel<HQ_BITS, CT, GS, SWI>), grid, dim3(256), 0, a.stream, k);
   return hipGetLastError();
+}
+
+template <bool SWI>
+hipError_t run_gqmm_g(const QArgs& a) {
+  const bool bf = a.xdt == DT_BF16;
+  switch (a.group_size) {
+    case 32: return bf ? run_gqmm<DT_BF16, 32, SWI>(a) : run_gqmm<DT_F16, 32, SWI>(a);
+    case 64: return bf ? run_gqmm<DT_BF16, 64, SWI>(a) : run_gqmm<DT_F16, 64, SWI>(a);
+    default: return bf ? run_gqmm<DT_BF16, 128, SWI>(a) : run_gqmm<DT_F16, 128, SWI>(a);
+  }
 }
 
 }  // namespace
@@ -687,12 +759,7 @@ hipError_t run_gqmm(const QArgs& a) {
 hipError_t HQ_CAT(launch_gqmm_t_b, HQ_BITS)(const QArgs& a) {
   if (a.xdt != a.sdt || a.xdt == DT_F32 || a.K % GBK != 0 || a.w_batch + 1 > 65535 || !a.rhs)
     return hipErrorNotSupported;
-  const bool bf = a.xdt == DT_BF16;
-  switch (a.group_size) {
-    case 32: return bf ? run_gqmm<DT_BF16, 32>(a) : run_gqmm<DT_F16, 32>(a);
-    case 64: return bf ? run_gqmm<DT_BF16, 64>(a) : run_gqmm<DT_F16, 64>(a);
-    default: return bf ? run_gqmm<DT_BF16, 128>(a) : run_gqmm<DT_F16, 128>(a);
-  }
+  return a.w2 ? run_gqmm_g<true>(a) : run_gqmm_g<false>(a);
 }
 
 template <int XDT, int SDT>
@@ -711,10 +778,15 @@ static void run_qmm_t(const QArgs& a) {
 hipError_t HQ_CAT(launch_qmm_t_b, HQ_BITS)(const QArgs& a) {
   // One product with same-type 16-bit x and scales, K a multiple of the step:
   // the large-tile GEMM. Everything else: the general batched kernel.
+  // (the large-tile GEMM addresses x and W with 32-bit element offsets)
+  const bool off32 = a.M * a.K < ((int64_t)1 << 31) &&
+                     a.N * (a.K / 32) * HQ_BITS < ((int64_t)1 << 31);
   if (a.batch == 1 && !a.lhs && !a.rhs && a.xdt == a.sdt && a.xdt != DT_F32 &&
-      a.K % GBK == 0 && a.M >= 128) {
+      a.K % GBK == 0 && a.M >= 128 && off32) {
+    if (a.w2) return a.xdt == DT_BF16 ? run_qgemm_g<DT_BF16, true>(a) : run_qgemm_g<DT_F16, true>(a);
     return a.xdt == DT_BF16 ? run_qgemm_g<DT_BF16>(a) : run_qgemm_g<DT_F16>(a);
   }
+  if (a.w2) return hipErrorNotSupported;  // fused SwiGLU: large-tile GEMM only
   switch (a.xdt * 3 + a.sdt) {
     case DT_F32 * 3 + DT_F32: run_qmm_t<DT_F32, DT_F32>(a); break;
     case DT_F32 * 3 + DT_F16: run_qmm_t<DT_F32, DT_F16>(a); break;

@@ -329,6 +329,11 @@ struct PKern {
   int M, N, K;
   int R;        // rounds per tile
   int ntiles;   // ceil(N / 16)
+  // SwiGLU: up projection (gate is w/s/b); a tile's gate rounds run first,
+  // then its up rounds, and the up finish combines both.
+  const uint32_t* w2;
+  const void* s2;
+  const void* b2;
   // 0x000F000F and the operand offset pair, passed as kernel arguments so the
   // compiler keeps them in registers and emits one v_and_or_b32 per pair (gfx9
   // VOP3 cannot encode 32-bit literals).
@@ -376,14 +381,20 @@ struct PCfg {
   static_assert(S % SU == 0, "segments per round must fill whole accumulators");
 };
 
-template <int BITS, int XDT, int SDT, int MB, int GS, int S>
+// DX (direct x): the A fragments come straight from global memory into the
+// round's registers (each lane loads the 32 x values of its own slot, the
+// rest of its A operand is zero), so there is no x staging in LDS and no
+// block barrier before the first MFMA; the group sums X come from one extra
+// MFMA per accumulator and k-step against an all-ones B operand.
+template <int BITS, int XDT, int SDT, int MB, int GS, int S, bool DX>
 struct RoundRegs {
   using C = PCfg<BITS, XDT, SDT, MB, GS, S>;
   uint32_t wd[S][BITS];
   float sv[C::NB][C::NG], bv[C::NB][C::NG];
+  u32x4 xv[DX ? C::NB : 1][DX ? 4 : 1];
 };
 
-template <int BITS, int XDT, int SDT, int MB, int GS, int S>
+template <int BITS, int XDT, int SDT, int MB, int GS, int S, bool DX, bool SWI>
 __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
   using C = PCfg<BITS, XDT, SDT, MB, GS, S>;
   using XS = st_t<XDT>;
@@ -391,7 +402,7 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
   constexpr int ODT = result_dtype(XDT, SDT);
   using OS = st_t<ODT>;
   using T = XMma<XDT>;
-  using Regs = RoundRegs<BITS, XDT, SDT, MB, GS, S>;
+  using Regs = RoundRegs<BITS, XDT, SDT, MB, GS, S, DX>;
   constexpr float OFF = kExact8<BITS, XDT> ? 0.f : T::OFF;
   constexpr int Z = C::Z, SU = C::SU, NB = C::NB, NSLOT = C::NSLOT, NG = C::NG;
 
@@ -404,9 +415,10 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
   const int64_t G = K / GS;
 
   // LDS: x rows [M][K] | 64 B of zeros | X sums [G][MB] | red [2][W][MB][16]
-  const int zoff = M * K * 2;
+  // (| gate sums [MB][16] with SWI); with DX no x rows, zeros or X sums.
+  const int zoff = DX ? 0 : M * K * 2;
   float* Xs = reinterpret_cast<float*>(smem + zoff + 64);
-  float* red = Xs + G * MB;
+  float* red = DX ? reinterpret_cast<float*>(smem) : Xs + G * MB;
 
   const int nl = lane & 15, q = lane >> 4;
   // A side: this lane supplies x row mA of slot sigA for k-block q.
@@ -439,43 +451,93 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
     }
   };
 
-  auto issue = [&](Regs& r, int t, int rnd) {
+  // Item rr of a tile: half hf = rr / R (1 = up projection, SWI only),
+  // round rr % R.
+  auto issue = [&](Regs& r, int t, int rr) {
+    const int hf = SWI ? (rr >= R ? 1 : 0) : 0;
+    const int rnd = rr - hf * R;
     const int n = min(t * 16 + nl, N - 1);
     const int seg_base = (rnd * W + wv) * S;
-    const uint32_t* wp = a.w + (int64_t)n * P + (int64_t)(seg_base * 4 + q) * BITS;
+    const uint32_t* wp = (hf ? a.w2 : a.w) + (int64_t)n * P + (int64_t)(seg_base * 4 + q) * BITS;
 #pragma unroll
     for (int u = 0; u < S; u++) load_pack<BITS>(wp + u * 4 * BITS, r.wd[u]);
-    const SS* sp = (const SS*)a.s + (int64_t)n * G + seg_base * Z + gsig;
-    const SS* bp = (const SS*)a.b + (int64_t)n * G + seg_base * Z + gsig;
+    const SS* sp = (const SS*)(hf ? a.s2 : a.s) + (int64_t)n * G + seg_base * Z + gsig;
+    const SS* bp = (const SS*)(hf ? a.b2 : a.b) + (int64_t)n * G + seg_base * Z + gsig;
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       load_groups<SDT, NG>(sp + j * NSLOT, r.sv[j]);
       load_groups<SDT, NG>(bp + j * NSLOT, r.bv[j]);
     }
+    if constexpr (DX) {
+      // x[mA, seg * 128 + q * 32 .. + 31] of this lane's slot; lanes without
+      // a slot load row 0 of the round's first segment and zero it later.
+      const int mx = validA ? mA : 0, ux = validA ? uA : 0;
+      const XS* xp = (const XS*)a.x + (int64_t)mx * K + (seg_base + ux) * 128 + q * 32;
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          r.xv[j][i] = *reinterpret_cast<const u32x4*>(xp + j * SU * 128 + i * 8);
+    }
   };
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const Regs& r, int rnd) {
+  auto compute = [&](const Regs& r, int rr) {
+    const int rnd = SWI ? (rr >= R ? rr - R : rr) : rr;
     const int seg_base = (rnd * W + wv) * S;
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       // the one segment of this accumulator whose A rows this lane fills
       const int real = xlane + (seg_base + j * SU + uA) * 256;
       floatx4 d = {0.f, 0.f, 0.f, 0.f};
+      u32x4 xa[4];
+      if constexpr (DX) {
+        // this lane's x in MFMA pair order (0,4,1,5,2,6,3,7), or zeros
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const u32x4 dd = r.xv[j][i];
+          xa[i][0] = validA ? ((dd[0] & 0xffffu) | (dd[2] << 16)) : 0u;
+          xa[i][1] = validA ? ((dd[0] >> 16) | (dd[2] & 0xffff0000u)) : 0u;
+          xa[i][2] = validA ? ((dd[1] & 0xffffu) | (dd[3] << 16)) : 0u;
+          xa[i][3] = validA ? ((dd[1] >> 16) | (dd[3] & 0xffff0000u)) : 0u;
+        }
+      }
 #pragma unroll
       for (int uu = 0; uu < SU; uu++) {
         const int addr = (validA && uA == uu) ? real : zoff;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const u32x4 bw = unpack(r.wd[j * SU + uu], i);
-          const u32x4 av = *reinterpret_cast<const u32x4*>(smem + addr + i * 16);
+          u32x4 av;
+          if constexpr (DX) {
+            const bool on = (uA == uu);
+            av[0] = on ? xa[i][0] : 0u;
+            av[1] = on ? xa[i][1] : 0u;
+            av[2] = on ? xa[i][2] : 0u;
+            av[3] = on ? xa[i][3] : 0u;
+          } else {
+            av = *reinterpret_cast<const u32x4*>(smem + addr + i * 16);
+          }
           d = T::mma(__builtin_bit_cast(typename T::frag, av),
                      __builtin_bit_cast(typename T::frag, bw), d);
         }
       }
-      const int g0 = seg_base * Z + j * NSLOT + gsig;
-      const floatx4 X = *reinterpret_cast<const floatx4*>(Xs + g0 * MB + md0);
+      floatx4 X;
+      if constexpr (DX) {
+        // X[row] = sum of that row's x over its group: A (every segment of
+        // the accumulator at once: a lane feeds exactly one) times ones.
+        constexpr uint32_t ONE2 = XDT == DT_BF16 ? 0x3F803F80u : 0x3C003C00u;
+        const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
+        X = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          X = T::mma(__builtin_bit_cast(typename T::frag, xa[i]),
+                     __builtin_bit_cast(typename T::frag, ones), X);
+      } else {
+        const int g0 = seg_base * Z + j * NSLOT + gsig;
+        X = *reinterpret_cast<const floatx4*>(Xs + g0 * MB + md0);
+      }
 #pragma unroll
       for (int v = 0; v < 4; v++) {
         const int gi = NG == 4 ? v : (NG == 2 ? v / 2 : 0);
@@ -493,7 +555,7 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
   for (int v = 0; v < 4; v++) keep[v] = ((4 * q + v) / MB < NSLOT) ? 1.f : 0.f;
   constexpr int MV = MB < 4 ? MB : 4;  // distinct x rows per lane
 
-  auto finish_tile = [&](int t, int buf) {
+  auto finish_tile = [&](int t, int hf, int buf) {
     // 1) fold this lane's values onto its x rows, 2) sum over the lane groups
     //    that hold other slots of the same rows, 3) one LDS slot per wave.
     float part[MV];
@@ -528,6 +590,15 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
       const int m = e >> 4, n = e & 15;
       float sum = 0.f;
       for (int w2 = 0; w2 < W; w2++) sum += rb[(w2 * MB + m) * 16 + n];
+      if constexpr (SWI) {
+        // the same thread handles element e in the gate and the up finish
+        float* gsum = red + 2 * W * 16 * MB;
+        if (hf == 0) {
+          gsum[e] = sum;
+          continue;
+        }
+        sum = swiglu_f32(DT_<ODT>::round(gsum[e]), DT_<ODT>::round(sum));
+      }
       if (t * 16 + n < N) ((OS*)a.y)[(int64_t)m * N + t * 16 + n] = DT_<ODT>::from_f32(sum);
     }
   };
@@ -565,35 +636,40 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
     if ((c & (GS / 8 - 1)) == 0) Xs[(c / (GS / 8)) * MB + m] = sum;
   };
   const int bd = blockDim.x;
-  u32x4 xd0 = {0u, 0u, 0u, 0u}, xd1 = {0u, 0u, 0u, 0u};
-  if (tid < items) xd0 = xload(tid);
-  if (tid + bd < items) xd1 = xload(tid + bd);
-  issue(r0, t, 0);
-  if (tid < items) stage(tid, xd0);
-  if (tid + bd < items) stage(tid + bd, xd1);
-  for (int e = tid + 2 * bd; e < items; e += bd) stage(e, xload(e));
-  for (int e = tid; e < G * MB; e += bd)
-    if ((e % MB) >= M) Xs[e] = 0.f;
-  if (tid < 4) reinterpret_cast<u32x4*>(smem + zoff)[tid] = u32x4{0u, 0u, 0u, 0u};
-  __syncthreads();
+  if constexpr (DX) {
+    issue(r0, t, 0);
+  } else {
+    u32x4 xd0 = {0u, 0u, 0u, 0u}, xd1 = {0u, 0u, 0u, 0u};
+    if (tid < items) xd0 = xload(tid);
+    if (tid + bd < items) xd1 = xload(tid + bd);
+    issue(r0, t, 0);
+    if (tid < items) stage(tid, xd0);
+    if (tid + bd < items) stage(tid + bd, xd1);
+    for (int e = tid + 2 * bd; e < items; e += bd) stage(e, xload(e));
+    for (int e = tid; e < G * MB; e += bd)
+      if ((e % MB) >= M) Xs[e] = 0.f;
+    if (tid < 4) reinterpret_cast<u32x4*>(smem + zoff)[tid] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+  }
 
-  // items (t, rnd) in order; buffers alternate, the next item's loads are
+  // items (t, rr) in order; buffers alternate, the next item's loads are
   // issued before the current item is computed
+  const int RH = SWI ? 2 * R : R;
   int buf = 0;
   while (true) {
     if (t >= a.ntiles) break;
     int t1 = t, r1n = rnd + 1;
-    if (r1n == R) { r1n = 0; t1 += step; }
+    if (r1n == RH) { r1n = 0; t1 += step; }
     if (t1 < a.ntiles) issue(r1, t1, r1n);
     compute(r0, rnd);
-    if (rnd == R - 1) { finish_tile(t, buf); buf ^= 1; }
+    if (rnd == R - 1 || rnd == RH - 1) { finish_tile(t, rnd >= R, buf); buf ^= 1; }
     t = t1; rnd = r1n;
     if (t >= a.ntiles) break;
     t1 = t; r1n = rnd + 1;
-    if (r1n == R) { r1n = 0; t1 += step; }
+    if (r1n == RH) { r1n = 0; t1 += step; }
     if (t1 < a.ntiles) issue(r0, t1, r1n);
     compute(r1, rnd);
-    if (rnd == R - 1) { finish_tile(t, buf); buf ^= 1; }
+    if (rnd == R - 1 || rnd == RH - 1) { finish_tile(t, rnd >= R, buf); buf ^= 1; }
     t = t1; rnd = r1n;
   }
 }
@@ -611,39 +687,55 @@ int device_cus() {
   return cus;
 }
 
-// Launches the persistent kernel, or returns hipErrorNotSupported for shapes
-// it does not take (the caller then uses the blocked kernel).
-template <int XDT, int SDT, int MB, int GS, int S>
-hipError_t run_qmvp_s(const QArgs& a, int W, int R) {
-  using C = PCfg<HQ_BITS, XDT, SDT, MB, GS, S>;
-  const size_t G = (size_t)a.K / GS;
-  const size_t lds = (size_t)a.M * a.K * 2 + 64 + G * MB * 4 + (size_t)2 * W * 16 * MB * 4;
-  if (lds > 160 * 1024) return hipErrorNotSupported;
-  PKern k;
-  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
-  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K; k.R = R;
-  k.nib_mask = 0x000F000Fu;
-  k.off_pair = XMma<XDT>::OFFB;
-  const int ntiles = (int)((a.N + 15) / 16);
-  k.ntiles = ntiles;
-  auto fn = qmvp_kernel<HQ_BITS, XDT, SDT, MB, GS, S>;
-  // Blocks per CU: as many as LDS and registers keep resident at once (up to
-  // 4), so every block's tiles stream concurrently.
-  static int waves_per_simd = 0;
-  if (waves_per_simd == 0) {
-    hipFuncAttributes fa;
-    int vg = 128;
-    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)) == hipSuccess && fa.numRegs > 0)
-      vg = fa.numRegs;
-    waves_per_simd = vg <= 128 ? 4 : (vg <= 168 ? 3 : (vg <= 256 ? 2 : 1));
-  }
+// Bytes of LDS one block of the persistent kernel uses.
+inline size_t qmvp_lds(const QArgs& a, int W, int MB, int GS, bool dx, bool swi) {
+  const size_t red = (size_t)2 * W * 16 * MB * 4 + (swi ? (size_t)MB * 16 * 4 : 0);
+  if (dx) return red;
+  return (size_t)a.M * a.K * 2 + 64 + (size_t)(a.K / GS) * MB * 4 + red;
+}
+
+// Blocks per CU: as many as LDS and registers keep resident at once (up to
+// 4), so every block's tiles stream concurrently. Returns the grid size.
+inline int qmvp_grid(int ntiles, size_t lds, int vgprs, int W) {
+  const int waves_per_simd = vgprs <= 128 ? 4 : (vgprs <= 168 ? 3 : (vgprs <= 256 ? 2 : 1));
   int per_cu = (int)((160 * 1024) / lds);
   if (per_cu > 4) per_cu = 4;
   if (per_cu > (4 * waves_per_simd) / W) per_cu = (4 * waves_per_simd) / W;
   if (per_cu < 1) per_cu = 1;
   const int maxb = per_cu * device_cus();
   const int per = (ntiles + maxb - 1) / maxb;
-  const int grid = (ntiles + per - 1) / per;
+  return (ntiles + per - 1) / per;
+}
+
+template <int XDT, int SDT, int MB, int GS, int S, bool DX, bool SWI>
+int qmvp_vgprs() {
+  static int vg = 0;
+  if (vg == 0) {
+    hipFuncAttributes fa;
+    auto fn = qmvp_kernel<HQ_BITS, XDT, SDT, MB, GS, S, DX, SWI>;
+    vg = (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)) == hipSuccess && fa.numRegs > 0)
+             ? fa.numRegs : 128;
+  }
+  return vg;
+}
+
+// Launches the persistent kernel with W waves per block and R rounds per
+// tile, or returns hipErrorNotSupported when x does not fit LDS.
+template <int XDT, int SDT, int MB, int GS, int S, bool DX, bool SWI>
+hipError_t run_qmvp_s(const QArgs& a, int W, int R) {
+  using C = PCfg<HQ_BITS, XDT, SDT, MB, GS, S>;
+  const size_t lds = qmvp_lds(a, W, MB, GS, DX, SWI);
+  if (lds > 160 * 1024) return hipErrorNotSupported;
+  PKern k;
+  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
+  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K; k.R = R;
+  k.nib_mask = 0x000F000Fu;
+  k.off_pair = XMma<XDT>::OFFB;
+  k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
+  const int ntiles = (int)((a.N + 15) / 16);
+  k.ntiles = ntiles;
+  auto fn = qmvp_kernel<HQ_BITS, XDT, SDT, MB, GS, S, DX, SWI>;
+  const int grid = qmvp_grid(ntiles, lds, qmvp_vgprs<XDT, SDT, MB, GS, S, DX, SWI>(), W);
   static bool big_lds = false;
   if (lds > 64 * 1024 && !big_lds) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -656,7 +748,37 @@ hipError_t run_qmvp_s(const QArgs& a, int W, int R) {
   return hipGetLastError();
 }
 
-template <int XDT, int SDT, int MB, int GS>
+// Direct x only where the round buffers stay within registers: per buffer a
+// lane holds NB * 4 x fragments (16 VGPRs each accumulator), S * BITS weight
+// words and 2 * NB * NG scale/bias values; two buffers and ~50 more VGPRs
+// must fit 256.
+template <int MB, int GS, int S>
+constexpr bool kDirectOk = PCfg<HQ_BITS, DT_BF16, DT_BF16, MB, GS, S>::NB * 16 + S * HQ_BITS +
+                               2 * PCfg<HQ_BITS, DT_BF16, DT_BF16, MB, GS, S>::NB *
+                                   PCfg<HQ_BITS, DT_BF16, DT_BF16, MB, GS, S>::NG <= 100;
+
+// Staged x is loaded once per block and reused by every tile the block
+// walks; direct x is reloaded per tile but needs no LDS and no barrier
+// before the first MFMA. Direct x is used when x does not fit LDS, or for
+// M >= 2 when every block gets one tile both ways (direct x holds more
+// registers, which can lower the blocks per CU). At M = 1 staging measured
+// as fast or faster on every Llama-3-8B decode shape.
+template <int XDT, int SDT, int MB, int GS, int S, bool SWI>
+hipError_t run_qmvp_sd(const QArgs& a, int W, int R) {
+  if constexpr (kDirectOk<MB, GS, S>) {
+    const size_t lds = qmvp_lds(a, W, MB, GS, false, SWI);
+    const int ntiles = (int)((a.N + 15) / 16);
+    if (lds > 160 * 1024 ||
+        (a.M >= 2 &&
+         qmvp_grid(ntiles, lds, qmvp_vgprs<XDT, SDT, MB, GS, S, false, SWI>(), W) >= ntiles &&
+         qmvp_grid(ntiles, qmvp_lds(a, W, MB, GS, true, SWI),
+                   qmvp_vgprs<XDT, SDT, MB, GS, S, true, SWI>(), W) >= ntiles))
+      return run_qmvp_s<XDT, SDT, MB, GS, S, true, SWI>(a, W, R);
+  }
+  return run_qmvp_s<XDT, SDT, MB, GS, S, false, SWI>(a, W, R);
+}
+
+template <int XDT, int SDT, int MB, int GS, bool SWI>
 hipError_t run_qmvp(const QArgs& a) {
   constexpr int Z = 128 / GS;
   if constexpr (Z * MB > 16) {
@@ -667,19 +789,21 @@ hipError_t run_qmvp(const QArgs& a) {
     const int ntiles = (int)((a.N + 15) / 16);
     // S = 8 segments per round and W <= 8 waves with W * 8 dividing nseg.
     // When that leaves fewer than 8 waves per tile and tiles are few (small
-    // N), rounds of S = 4 give each tile up to twice the waves.
+    // N), rounds of S = 4 give each tile up to twice the waves. Rounds of
+    // S = 4 also serve x that does not fit LDS when direct x at S = 8 would
+    // spill registers.
     auto pick = [&](int S) {
       for (int c = 8; c >= 1; c--)
         if ((nseg / S) % c == 0) return c;
       return 0;
     };
-    const int W8 = pick(8);
-    if (W8 < 8 && ntiles <= 512) {
-      const int W4 = pick(4);
-      if (W4 > W8) return run_qmvp_s<XDT, SDT, MB, GS, 4>(a, W4, nseg / (4 * W4));
-    }
+    const int W8 = pick(8), W4 = pick(4);
+    if (W8 < 8 && ntiles <= 512 && W4 > W8)
+      return run_qmvp_sd<XDT, SDT, MB, GS, 4, SWI>(a, W4, nseg / (4 * W4));
     if (W8 == 0) return hipErrorNotSupported;
-    return run_qmvp_s<XDT, SDT, MB, GS, 8>(a, W8, nseg / (8 * W8));
+    if (!kDirectOk<MB, GS, 8> && qmvp_lds(a, W8, MB, GS, false, SWI) > 160 * 1024)
+      return run_qmvp_sd<XDT, SDT, MB, GS, 4, SWI>(a, W4, nseg / (4 * W4));
+    return run_qmvp_sd<XDT, SDT, MB, GS, 8, SWI>(a, W8, nseg / (8 * W8));
   }
 }
 
@@ -718,30 +842,36 @@ hipError_t run_qmvx(const QArgs& a) {
   return hipGetLastError();
 }
 
-template <int XDT, int SDT, int MB, int GS>
+template <int XDT, int SDT, int MB, int GS, bool SWI>
 hipError_t run_qmvx_any(const QArgs& a) {
-  if (a.batch == 1 && !a.lhs && !a.rhs) {
-    hipError_t e = run_qmvp<XDT, SDT, MB, GS>(a);
-    if (e != hipErrorNotSupported) return e;
+  if constexpr (SWI) {
+    // fused SwiGLU: persistent kernel only (batch 1, K % 1024 == 0)
+    if (a.batch != 1 || a.lhs || a.rhs) return hipErrorNotSupported;
+    return run_qmvp<XDT, SDT, MB, GS, true>(a);
+  } else {
+    if (a.batch == 1 && !a.lhs && !a.rhs) {
+      hipError_t e = run_qmvp<XDT, SDT, MB, GS, false>(a);
+      if (e != hipErrorNotSupported) return e;
+    }
+    return run_qmvx<XDT, SDT, MB, GS>(a);
   }
-  return run_qmvx<XDT, SDT, MB, GS>(a);
 }
 
-template <int XDT, int SDT, int MB>
+template <int XDT, int SDT, int MB, bool SWI>
 hipError_t run_qmvx_g(const QArgs& a) {
   switch (a.group_size) {
-    case 32: return run_qmvx_any<XDT, SDT, MB, 32>(a);
-    case 64: return run_qmvx_any<XDT, SDT, MB, 64>(a);
-    default: return run_qmvx_any<XDT, SDT, MB, 128>(a);
+    case 32: return run_qmvx_any<XDT, SDT, MB, 32, SWI>(a);
+    case 64: return run_qmvx_any<XDT, SDT, MB, 64, SWI>(a);
+    default: return run_qmvx_any<XDT, SDT, MB, 128, SWI>(a);
   }
 }
 
-template <int XDT, int SDT>
+template <int XDT, int SDT, bool SWI = false>
 hipError_t run_qmvx_m(const QArgs& a) {
-  if (a.M <= 1) return run_qmvx_g<XDT, SDT, 1>(a);
-  if (a.M <= 2) return run_qmvx_g<XDT, SDT, 2>(a);
-  if (a.M <= 4) return run_qmvx_g<XDT, SDT, 4>(a);
-  return run_qmvx_g<XDT, SDT, 8>(a);
+  if (a.M <= 1) return run_qmvx_g<XDT, SDT, 1, SWI>(a);
+  if (a.M <= 2) return run_qmvx_g<XDT, SDT, 2, SWI>(a);
+  if (a.M <= 4) return run_qmvx_g<XDT, SDT, 4, SWI>(a);
+  return run_qmvx_g<XDT, SDT, 8, SWI>(a);
 }
 
 }  // namespace
@@ -750,6 +880,12 @@ hipError_t run_qmvx_m(const QArgs& a) {
 #define HQ_CAT(a, b) HQ_CAT_(a, b)
 
 hipError_t HQ_CAT(launch_qmvx_t_b, HQ_BITS)(const QArgs& a) {
+  if (a.w2) {
+    // fused SwiGLU: x and scales of one 16-bit dtype
+    if (a.xdt == DT_BF16 && a.sdt == DT_BF16) return run_qmvx_m<DT_BF16, DT_BF16, true>(a);
+    if (a.xdt == DT_F16 && a.sdt == DT_F16) return run_qmvx_m<DT_F16, DT_F16, true>(a);
+    return hipErrorNotSupported;
+  }
   switch (a.xdt * 3 + a.sdt) {
     case DT_BF16 * 3 + DT_BF16: return run_qmvx_m<DT_BF16, DT_BF16>(a);
     case DT_BF16 * 3 + DT_F16: return run_qmvx_m<DT_BF16, DT_F16>(a);

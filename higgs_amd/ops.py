@@ -11,6 +11,12 @@ same argument names, meanings and validation messages:
   higgs' ``gather_qmm`` (qwen3_next.rs:509-578).
 * ``dequantize(w, scales, biases, group_size, bits)`` -- mlx-rs
   ``ops::dequantize`` (qwen3_next.rs:314).
+* ``dense_hidden_fused`` -- ``FfnBlock::dense_hidden_fused``
+  (qwen3_next.rs:2539-2585): gate/up projection and SwiGLU in one launch.
+* ``forward_gather_global_sort`` / ``moe_block`` -- the MoE experts on the
+  global-sort path (qwen3_next.rs:1731-1809; qwen3_moe.rs:353-357), from the
+  building blocks ``moe_sort``, ``gather_qmm_swiglu``, ``gather_qmm`` and
+  ``moe_combine``.
 
 Tensors are torch tensors on the GPU: torch provides device memory and the
 current HIP stream, and the arithmetic runs in libhiggs_qmm.so. Packed weights
@@ -297,3 +303,217 @@ def embedding(indices: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
         _ptr(out), _ptr(w), _ptr(scales), _ptr(biases), _ptr(flat), flat.numel(), w.shape[0], K,
         group_size, bits, _DT[scales.dtype], _stream(dev)))
     return out
+
+
+# --- fused SwiGLU and the MoE global-sort block ---------------------------------
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """gate * sigmoid(gate) * up, elementwise (qwen3_next.rs:340-342)."""
+    tag = "swiglu"
+    dev = _check_device(tag, gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype or gate.dtype not in _DT:
+        raise _err(f"[{tag}] gate and up must be float arrays of one shape and dtype (got "
+                   f"{_shape(gate)} {_dt_name(gate)} and {_shape(up)} {_dt_name(up)}).")
+    gate, up = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(gate)
+    if out.numel():
+        _lib.check(_lib.lib().hq_swiglu(_ptr(out), _ptr(gate), _ptr(up), out.numel(),
+                                        _DT[gate.dtype], _stream(dev)))
+    return out
+
+
+def _split_rows(t: torch.Tensor, n: int):
+    return t[..., :n, :], t[..., n:, :]
+
+
+def dense_hidden_fused(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                       biases: torch.Tensor, intermediate: int, group_size: int = 64,
+                       bits: int = 4) -> torch.Tensor:
+    """swiglu of a gate/up projection pair stored concatenated along N.
+
+    higgs' FfnBlock::dense_hidden_fused (crates/higgs-models/src/qwen3_next.rs:
+    2539-2585): ``w``/``scales``/``biases`` are gate_proj and up_proj
+    concatenated on axis 0 ([2*intermediate, P]); the result is
+    silu_mul(split(x @ deq(w).T, intermediate)) of shape [..., intermediate].
+    Gate and up run in one launch with the SwiGLU in the epilogue; shapes the
+    fused kernel does not take run as two quantized_matmul calls and
+    ``swiglu``.
+    """
+    tag = "quantized_matmul_swiglu"
+    _check_params(tag, group_size, bits)
+    w, w_inner, w_outer = _extract_dims(tag, x, w, scales, biases, True, group_size, bits)
+    if w.dim() != 2 or w_outer != 2 * intermediate or intermediate <= 0:
+        raise _err(f"[{tag}] The fused weight must be [2*intermediate, P] = "
+                   f"[{2 * intermediate}, ...] (got {_shape(w)}).")
+    dev = _check_device(tag, x, w, scales, biases)
+    wg, wu = _split_rows(w, intermediate)
+    sg, su = _split_rows(scales.contiguous(), intermediate)
+    bg, bu = _split_rows(biases.contiguous(), intermediate)
+    return swiglu_pair(x, (wg, sg, bg), (wu, su, bu), group_size, bits, dev=dev)
+
+
+def swiglu_pair(x: torch.Tensor, gate: Sequence[torch.Tensor], up: Sequence[torch.Tensor],
+                group_size: int = 64, bits: int = 4, dev=None) -> torch.Tensor:
+    """swiglu(x @ deq(Wg).T, x @ deq(Wu).T) for separate (w, scales, biases)
+    triples of equal shape; x is [..., K], the result [..., N]."""
+    tag = "quantized_matmul_swiglu"
+    wg, sg, bg = gate
+    wu, su, bu = up
+    _check_params(tag, group_size, bits)
+    wg, K, N = _extract_dims(tag, x, wg, sg, bg, True, group_size, bits)
+    wu, _, _ = _extract_dims(tag, x, wu, su, bu, True, group_size, bits)
+    if wg.shape != wu.shape or wg.dim() != 2 or sg.dtype != su.dtype:
+        raise _err(f"[{tag}] gate and up projections must be 2-D with one shape and dtype.")
+    dev = dev or _check_device(tag, x, wg, sg, bg, wu, su, bu)
+    sg, bg, su, bu = (t.contiguous() for t in (sg, bg, su, bu))
+    x = x.contiguous()
+    out_dtype = result_dtype(x.dtype, sg.dtype)
+    h = torch.empty((*x.shape[:-1], N), dtype=out_dtype, device=dev)
+    M = x.numel() // K if K else 0
+    if h.numel() == 0:
+        return h
+    rc = _lib.lib().hq_quantized_matmul_swiglu(
+        _ptr(h), _ptr(x), _ptr(wg), _ptr(sg), _ptr(bg), _ptr(wu), _ptr(su), _ptr(bu),
+        M, N, K, group_size, bits, _DT[x.dtype], _DT[sg.dtype], _stream(dev))
+    if rc == _lib.HQ_ERR_UNSUPPORTED:
+        g = quantized_matmul(x, wg, sg, bg, True, group_size, bits)
+        u = quantized_matmul(x, wu, su, bu, True, group_size, bits)
+        return swiglu(g, u)
+    _lib.check(rc)
+    return h
+
+
+def gather_qmm_swiglu(x: torch.Tensor, gate: Sequence[torch.Tensor], up: Sequence[torch.Tensor],
+                      lhs_indices: Optional[torch.Tensor], rhs_indices: torch.Tensor,
+                      group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """swiglu(gather_qmm(x, Wg, ...), gather_qmm(x, Wu, ...)) on the sorted path.
+
+    The gate/up pair and SwiGLU of SwitchMlpWeights::forward_gather_global_sort
+    (crates/higgs-models/src/qwen3_next.rs:1764-1787) in one launch. x is
+    [x_batch, M, K]; Wg/Wu [E, N, P]; rhs_indices are flat, non-decreasing
+    expert ids; lhs_indices (optional, flat) pick x's batch element per row.
+    Returns [batch, M, N].
+    """
+    tag = "gather_qmm_swiglu"
+    wg, sg, bg = gate
+    wu, su, bu = up
+    _check_params(tag, group_size, bits)
+    wg, K, N = _extract_dims(tag, x, wg, sg, bg, True, group_size, bits)
+    wu, _, _ = _extract_dims(tag, x, wu, su, bu, True, group_size, bits)
+    if wg.shape != wu.shape or wg.dim() != 3:
+        raise _err(f"[{tag}] gate and up weights must both be [E, N, P] (got {_shape(wg)} and "
+                   f"{_shape(wu)}).")
+    dev = _check_device(tag, x, wg, sg, bg, wu, su, bu, lhs_indices, rhs_indices)
+    rhs = _as_u32_indices(tag, rhs_indices, "rhs_indices").reshape(-1)
+    lhs = None if lhs_indices is None else _as_u32_indices(tag, lhs_indices, "lhs_indices").reshape(-1)
+    if lhs is not None and lhs.numel() != rhs.numel():
+        raise _err(f"[{tag}] lhs_indices and rhs_indices must have one length.")
+    x = x.contiguous()
+    x_batch = x.numel() // (x.shape[-2] * K) if x.numel() else 1
+    M = x.shape[-2]
+    batch = rhs.numel()
+    h = torch.empty((batch, M, N), dtype=result_dtype(x.dtype, sg.dtype), device=dev)
+    if h.numel() == 0:
+        return h
+    _lib.check(_lib.lib().hq_gather_qmm_swiglu(
+        _ptr(h), _ptr(x), _ptr(wg), _ptr(sg.contiguous()), _ptr(bg.contiguous()), _ptr(wu),
+        _ptr(su.contiguous()), _ptr(bu.contiguous()), _ptr(lhs), _ptr(rhs), batch,
+        max(x_batch, 1), wg.shape[0], M, N, K, group_size, bits, _DT[x.dtype], _DT[sg.dtype],
+        _stream(dev)))
+    return h
+
+
+def moe_sort(indices: torch.Tensor, num_experts: int):
+    """The index plumbing of forward_gather_global_sort (qwen3_next.rs:1746-1761).
+
+    indices: [..., top_k] expert ids. Returns (order, inv_order, idx_sorted,
+    token_idx), each int32 [n] (uint32 bit patterns), n = indices.numel():
+    order = stable argsort of the flattened ids, inv_order = argsort(order),
+    idx_sorted = ids[order], token_idx = order // top_k.
+    """
+    tag = "moe_sort"
+    dev = _check_device(tag, indices)
+    if indices.dim() < 1:
+        raise _err(f"[{tag}] indices must have a top_k axis.")
+    top_k = indices.shape[-1]
+    flat = _as_u32_indices(tag, indices, "indices").reshape(-1)
+    n = flat.numel()
+    outs = [torch.empty(n, dtype=torch.int32, device=dev) for _ in range(4)]
+    if n:
+        _lib.check(_lib.lib().hq_moe_sort(*(_ptr(o) for o in outs), _ptr(flat), n, top_k,
+                                          num_experts, _stream(dev)))
+    return tuple(outs)
+
+
+def moe_combine(y_sorted: torch.Tensor, inv_order: torch.Tensor,
+                scores: torch.Tensor) -> torch.Tensor:
+    """out[t] = sum_j scores[t, j] * y_sorted[inv_order[t*top_k + j]].
+
+    The unsort of forward_gather_global_sort (qwen3_next.rs:1802-1808) fused
+    with the score-weighted sum of the MoE block (qwen3_moe.rs:355-357).
+    y_sorted: [n, D] (or [n, 1, D]); scores: [..., top_k]; returns
+    scores.shape[:-1] + [D].
+    """
+    tag = "moe_combine"
+    dev = _check_device(tag, y_sorted, inv_order, scores)
+    top_k = scores.shape[-1]
+    tokens = scores.numel() // top_k if top_k else 0
+    D = y_sorted.shape[-1]
+    y = y_sorted.contiguous().reshape(-1, D)
+    inv = _as_u32_indices(tag, inv_order, "inv_order").reshape(-1)
+    if y.shape[0] != tokens * top_k or inv.numel() != tokens * top_k:
+        raise _err(f"[{tag}] y_sorted has {y.shape[0]} rows and inv_order {inv.numel()} for "
+                   f"{tokens} tokens x top_k {top_k}.")
+    if y.dtype not in _DT or scores.dtype not in _DT:
+        raise _err(f"[{tag}] y and scores must be float arrays.")
+    out = torch.empty((*scores.shape[:-1], D), dtype=y.dtype, device=dev)
+    if out.numel():
+        _lib.check(_lib.lib().hq_moe_combine(
+            _ptr(out), _ptr(y), _ptr(inv), _ptr(scores.contiguous()), tokens, top_k, D,
+            _DT[y.dtype], _DT[scores.dtype], _stream(dev)))
+    return out
+
+
+def _switch_sorted(x, indices, gate, up, down, group_size, bits):
+    """Sort, fused gate/up + SwiGLU, down; returns (y_sorted [n, D], inv_order)."""
+    wg = gate[0]
+    E = wg.shape[0]
+    D = x.shape[-1]
+    order, inv, srt, tok = moe_sort(indices, E)
+    xf = x.reshape(-1, 1, D)
+    h = gather_qmm_swiglu(xf, gate, up, tok, srt, group_size, bits)        # [n, 1, I]
+    y = gather_qmm(h, down[0], down[1], down[2], None, srt, True, group_size, bits, True)
+    return y.reshape(-1, y.shape[-1]), inv
+
+
+def forward_gather_global_sort(x: torch.Tensor, indices: torch.Tensor,
+                               gate: Sequence[torch.Tensor], up: Sequence[torch.Tensor],
+                               down: Sequence[torch.Tensor], group_size: int = 64,
+                               bits: int = 4) -> torch.Tensor:
+    """SwitchMlpWeights::forward_gather_global_sort (qwen3_next.rs:1731-1809).
+
+    x: [B, L, D]; indices: [B, L, top_k]; gate/up/down: (w, scales, biases)
+    of SwitchLinear weights [E, N, P]. Returns [B, L, top_k, D] in the
+    original (unsorted) order. The x gather rides on gather_qmm's
+    lhs_indices, gate/up/SwiGLU is one launch, and the unsort is a combine
+    with unit scores (an exact row copy).
+    """
+    B, L, D = x.shape
+    top_k = indices.shape[-1]
+    y, inv = _switch_sorted(x, indices, gate, up, down, group_size, bits)
+    ones = torch.ones((y.shape[0], 1), dtype=y.dtype, device=y.device)
+    out = moe_combine(y, inv, ones)
+    return out.reshape(B, L, top_k, -1)
+
+
+def moe_block(x: torch.Tensor, indices: torch.Tensor, scores: torch.Tensor,
+              gate: Sequence[torch.Tensor], up: Sequence[torch.Tensor],
+              down: Sequence[torch.Tensor], group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """Experts of the MoE block after routing (qwen3_moe.rs:353-357):
+    forward_gather_global_sort(x, indices) * scores, summed over top_k.
+
+    x: [B, L, D]; indices, scores: [B, L, top_k]. Returns [B, L, D]. Four
+    launches: sort, gate/up + SwiGLU, down, unsort + weighted sum.
+    """
+    y, inv = _switch_sorted(x, indices, gate, up, down, group_size, bits)
+    return moe_combine(y, inv, scores)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define HQ_ABI_VERSION 1
+#define HQ_ABI_VERSION 2
 
 typedef enum hq_status {
   HQ_OK = 0,
@@ -152,6 +152,109 @@ int hq_embedding_dequantize(void* out, const uint32_t* w, const void* scales,
                             const void* biases, const uint32_t* indices,
                             int64_t n, int64_t rows, int64_t K, int group_size,
                             int bits, int s_dtype, void* stream);
+
+/*
+ * Fused gate/up projection and SwiGLU of a dense MLP:
+ *   h = swiglu(x . deq(Wg)^T, x . deq(Wu)^T),  swiglu(g, u) = g * sigmoid(g) * u.
+ *
+ * Replaces higgs' FfnBlock::dense_hidden_fused (crates/higgs-models/src/
+ * qwen3_next.rs:2539-2585): one quantized_matmul over gate and up
+ * concatenated along N, split at N, then silu_mul (qwen3_next.rs:437-452;
+ * swiglu at 340-342). Here both projections run in one launch and the
+ * elementwise op is applied in the kernel's epilogue, so the [M, 2N]
+ * intermediate never reaches HBM. The gate and up matrices may be two
+ * halves of one concatenated buffer (w_up = w_gate + N*K*bits/32 words) or
+ * separate buffers.
+ *
+ *   x: [M, K]; w_gate, w_up: [N, K*bits/32]; s_*, b_*: [N, K/group_size];
+ *   h: [M, N] of x_dtype.
+ *
+ * Rounding: gate and up are each rounded to x_dtype (as the reference
+ * materialises them), swiglu is evaluated in float32 and rounded once.
+ * Supported: x_dtype == s_dtype in {float16, bfloat16}, and either
+ * M <= 127 with K a multiple of 1024, or M >= 128 with K a multiple of 64.
+ * Other shapes return HQ_ERR_UNSUPPORTED; callers then use
+ * hq_quantized_matmul for both halves and hq_swiglu.
+ */
+int hq_quantized_matmul_swiglu(void* h, const void* x, const uint32_t* w_gate,
+                               const void* s_gate, const void* b_gate,
+                               const uint32_t* w_up, const void* s_up,
+                               const void* b_up, int64_t M, int64_t N,
+                               int64_t K, int group_size, int bits,
+                               int x_dtype, int s_dtype, void* stream);
+
+/*
+ * Fused gate/up gather_qmm and SwiGLU of the MoE experts on the sorted path:
+ *   h[i] = swiglu(x[xi] . deq(Wg[wi])^T, x[xi] . deq(Wu[wi])^T)
+ * with xi, wi as in hq_gather_qmm.
+ *
+ * Replaces the gate_out / up_out gather_qmm pair and swiglu of
+ * SwitchMlpWeights::forward_gather_global_sort (crates/higgs-models/src/
+ * qwen3_next.rs:1764-1787). With lhs_indices = token_idx of hq_moe_sort the
+ * x_sorted gather (qwen3_next.rs:1754-1757) is fused too.
+ *
+ *   x: [x_batch, M, K]; w_gate, w_up: [w_batch, N, K*bits/32];
+ *   s_*, b_*: [w_batch, N, K/group_size]; h: [batch, M, N] of x_dtype.
+ *
+ * rhs_indices must be non-decreasing (sorted_indices semantics of
+ * hq_gather_qmm). Supported: x_dtype == s_dtype in {float16, bfloat16}, K a
+ * multiple of 64, w_batch < 65535; otherwise HQ_ERR_UNSUPPORTED. Rows with
+ * out-of-range indices are NaN. Rounding as hq_quantized_matmul_swiglu.
+ */
+int hq_gather_qmm_swiglu(void* h, const void* x, const uint32_t* w_gate,
+                         const void* s_gate, const void* b_gate,
+                         const uint32_t* w_up, const void* s_up,
+                         const void* b_up, const uint32_t* lhs_indices,
+                         const uint32_t* rhs_indices, int64_t batch,
+                         int64_t x_batch, int64_t w_batch, int64_t M,
+                         int64_t N, int64_t K, int group_size, int bits,
+                         int x_dtype, int s_dtype, void* stream);
+
+/*
+ * Elementwise out[i] = round(gate[i] * sigmoid(gate[i]) * up[i]), i < n,
+ * evaluated in float32 (gate, up, out of `dtype`).
+ *
+ * Replaces higgs' swiglu / silu_mul (crates/higgs-models/src/qwen3_next.rs:
+ * 340-342, 437-452) for the unfused paths.
+ */
+int hq_swiglu(void* out, const void* gate, const void* up, int64_t n,
+              int dtype, void* stream);
+
+/*
+ * Global expert sort of the MoE global-sort path.
+ *
+ * Replaces the index work of SwitchMlpWeights::forward_gather_global_sort
+ * (crates/higgs-models/src/qwen3_next.rs:1746-1761): with idx the flattened
+ * [tokens, top_k] expert indices (n = tokens * top_k),
+ *   order      = argsort(idx)   (stable: equal indices keep their order)
+ *   inv_order  = argsort(order) (inv_order[order[p]] = p)
+ *   idx_sorted = idx[order]     (non-decreasing)
+ *   token_idx  = order / top_k
+ * Any output may be NULL. Indices >= num_experts are placed after every
+ * valid one, in their original order (their gather_qmm rows are NaN).
+ * One workgroup does the sort; num_experts <= 2048, n < 2^31.
+ */
+int hq_moe_sort(uint32_t* order, uint32_t* inv_order, uint32_t* idx_sorted,
+                uint32_t* token_idx, const uint32_t* idx, int64_t n,
+                int64_t top_k, int64_t num_experts, void* stream);
+
+/*
+ * Unsort and score-weighted combine of the experts' outputs:
+ *   out[t, d] = sum_{j < top_k} round(scores[t, j] * y[inv_order[t*top_k + j], d])
+ * (summed in float32 in j order, rounded once to `dtype`).
+ *
+ * Replaces out_flat.take_axis(inv_order) and the reshape of
+ * forward_gather_global_sort (crates/higgs-models/src/qwen3_next.rs:
+ * 1802-1808) and the y * scores, sum over top_k of the MoE block
+ * (crates/higgs-models/src/qwen3_moe.rs:355-357).
+ *
+ *   y: [tokens*top_k, D] of dtype (rows in sorted order); inv_order: uint32
+ *   [tokens*top_k]; scores: [tokens, top_k] of score_dtype; out: [tokens, D].
+ * A row whose inv_order is out of range makes its token's output NaN.
+ */
+int hq_moe_combine(void* out, const void* y, const uint32_t* inv_order,
+                   const void* scores, int64_t tokens, int64_t top_k,
+                   int64_t D, int dtype, int score_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -65,6 +65,7 @@ def lib():
                                          _int, _int, _vp]
         L.hqo_gather_sort.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp]
         L.hqo_swiglu.argtypes = [_vp, _vp, _int, _i64, _vp]
+        L.hqo_moe_combine.argtypes = [_vp, _int, _vp, _vp, _int, _i64, _i64, _i64, _vp]
         L.hqo_num_threads.restype = _int
         _lib = L
     return _lib
@@ -228,6 +229,20 @@ def swiglu(gate: np.ndarray, up: np.ndarray, dtype: int) -> np.ndarray:
     up = np.ascontiguousarray(up)
     out = np.empty(gate.shape, gate.dtype)
     lib().hqo_swiglu(_p(gate), _p(up), dtype, gate.size, _p(out))
+    return out
+
+
+def moe_combine(y: np.ndarray, dtype: int, inv: np.ndarray, scores: np.ndarray,
+                sdtype: int) -> np.ndarray:
+    """out[t] = round(sum_j round(scores[t, j] * y[inv[t*k + j]])); y [n, D]
+    (bit patterns of dtype), scores [tokens, k]. Returns [tokens, D] of dtype."""
+    y = np.ascontiguousarray(y)
+    scores = np.ascontiguousarray(scores)
+    inv = np.ascontiguousarray(inv, dtype=np.uint32).reshape(-1)
+    tokens, top_k = scores.shape
+    D = y.shape[-1]
+    out = np.empty((tokens, D), y.dtype)
+    lib().hqo_moe_combine(_p(y), dtype, _p(inv), _p(scores), sdtype, tokens, top_k, D, _p(out))
     return out
 
 

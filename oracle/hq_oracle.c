@@ -411,3 +411,33 @@ void hqo_swiglu(const void* gate, const void* up, int dtype, int64_t n, void* ou
     store_dt(out, dtype, i, hqo_round_f64(g / (1.0 + exp(-g)) * u, dtype));
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* MoE unsort + score-weighted combine (qwen3_next.rs:1802-1808 take of     */
+/* inv_order; qwen3_moe.rs:355-357 y * scores summed over top_k)            */
+/* ------------------------------------------------------------------------ */
+
+/* out[t, d] = round(sum_j round(scores[t, j] * y[inv[t*k + j], d])): each
+ * product rounded to `dtype` (MLX's multiply of two `dtype` arrays), the sum
+ * over j in fp64, one final rounding. inv out of range -> NaN row. */
+void hqo_moe_combine(const void* y, int dtype, const uint32_t* inv, const void* scores,
+                     int sdtype, int64_t tokens, int64_t top_k, int64_t D, void* out) {
+  const int64_t rows = tokens * top_k;
+  for (int64_t t = 0; t < tokens; t++) {
+    int bad = 0;
+    for (int64_t j = 0; j < top_k; j++)
+      if ((int64_t)inv[t * top_k + j] >= rows) bad = 1;
+    for (int64_t d = 0; d < D; d++) {
+      double acc = 0.0;
+      if (!bad) {
+        for (int64_t j = 0; j < top_k; j++) {
+          const double sc = load_dt(scores, sdtype, t * top_k + j);
+          const double yv = load_dt(y, dtype, (int64_t)inv[t * top_k + j] * D + d);
+          acc += hqo_round_f64(sc * yv, dtype);
+        }
+      }
+      store_dt(out, dtype, t * D + d, bad ? (float)NAN : hqo_round_f64(acc, dtype));
+    }
+  }
+}
+

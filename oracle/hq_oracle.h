@@ -107,6 +107,12 @@ void hqo_gather_sort(const uint32_t* idx, int64_t n, int64_t top_k,
  * in double, rounded once to `dtype` (qwen3_next.rs:340-346). */
 void hqo_swiglu(const void* gate, const void* up, int dtype, int64_t n, void* out);
 
+/* MoE unsort + score-weighted combine (qwen3_next.rs:1802-1808,
+ * qwen3_moe.rs:355-357). y: [tokens*top_k, D] of dtype in sorted order;
+ * out: [tokens, D] of dtype. */
+void hqo_moe_combine(const void* y, int dtype, const uint32_t* inv, const void* scores,
+                     int sdtype, int64_t tokens, int64_t top_k, int64_t D, void* out);
+
 int hqo_num_threads(void);
 
 #ifdef __cplusplus

@@ -292,3 +292,56 @@ def test_splitmix64_published_vector():
         4593380528125082431, 16408922859458223821]
     assert [int(v) for v in gen.splitmix64(1234567, 2, offset=3)] == [
         4593380528125082431, 16408922859458223821]
+
+
+def _combine_case(seed, tokens, k, E, D):
+    idx = gen.topk_routing(seed, tokens, E, k)
+    order, inv, srt, tok = O.gather_sort(idx, k)
+    y = gen.np_x_bf16(seed + 1, (tokens * k, D))
+    return idx, order, inv, y
+
+
+def test_moe_combine_unit_scores_is_the_unsort(orc):
+    # top_k = 1 view with unit scores: out[i] = y_sorted[inv[i]] bit for bit, and
+    # with y_sorted = rows in sorted order this restores the original order.
+    idx, order, inv, y = _combine_case(3, 40, 4, 16, 24)
+    n = y.shape[0]
+    ones = np.full((n, 1), 0x3F80, np.uint16)              # bf16 1.0
+    out = orc.moe_combine(y, O.BF16, inv, ones, O.BF16)
+    np.testing.assert_array_equal(out, y[inv])
+    # sorted rows of an identity table come back as the row numbers
+    rows = orc.from_f32(np.repeat(np.arange(n, dtype=np.float32)[:, None], 2, 1), O.F32)
+    srt_rows = rows[order]
+    back = orc.moe_combine(srt_rows, O.F32, inv, np.ones((n, 1), np.float32), O.F32)
+    np.testing.assert_array_equal(back[:, 0], np.arange(n, dtype=np.float32))
+
+
+def test_moe_combine_one_hot_scores_pick_a_slot(orc):
+    idx, order, inv, y = _combine_case(5, 32, 4, 8, 16)
+    tokens, k = 32, 4
+    for j in range(k):
+        sc = np.zeros((tokens, k), np.float32)
+        sc[:, j] = 1.0
+        out = orc.moe_combine(y, O.BF16, inv, orc.from_f32(sc, O.BF16), O.BF16)
+        np.testing.assert_array_equal(out, y[inv.reshape(tokens, k)[:, j]])
+
+
+def test_moe_combine_weighted_sum_matches_float64(orc):
+    tokens, k, D = 64, 8, 48
+    idx, order, inv, y = _combine_case(11, tokens, k, 32, D)
+    sc = gen.np_x_bf16(12, (tokens, k))
+    out = gen.bf16_bits_to_f32(orc.moe_combine(y, O.BF16, inv, sc, O.BF16)).astype(np.float64)
+    yf = gen.bf16_bits_to_f32(y).astype(np.float64)
+    sf = gen.bf16_bits_to_f32(sc).astype(np.float64)
+    ref = (yf[inv].reshape(tokens, k, D) * sf[:, :, None]).sum(axis=1)
+    # products and the sum each round to bf16: within a few bf16 ulps of exact
+    assert np.abs(out - ref).max() <= 2 ** -6 * np.abs(yf).max() * np.abs(sf).max() * k
+
+
+def test_moe_combine_out_of_range_inv_gives_nan(orc):
+    y = gen.np_x_bf16(1, (8, 4))
+    inv = np.arange(8, dtype=np.uint32)
+    inv[5] = 99
+    sc = np.full((4, 2), 0x3F80, np.uint16)
+    out = gen.bf16_bits_to_f32(orc.moe_combine(y, O.BF16, inv, sc, O.BF16))
+    assert np.isnan(out[2]).all() and not np.isnan(np.delete(out, 2, 0)).any()
