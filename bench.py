@@ -21,7 +21,13 @@ Printed JSON line (one, on stdout):
   qmv_batch     the decode step at B = 1, 4, 8
   qmm           configs[2]: M = 2048 prefill GEMMs, TFLOP/s and fraction of
                 the 2.5 PFLOP/s dense bf16 MFMA peak
-  moe           configs[4]: sorted gather_qmm (gate, down) at the MoE shapes
+  moe           configs[4]: sorted gather_qmm (gate, down) at the MoE shapes,
+                and the whole expert block on device (sort, fused gate/up +
+                SwiGLU, down, unsort + score-weighted combine)
+  decode_fused  the same decode step with the launches fused: q|k|v
+                concatenated (one launch), gate/up + SwiGLU in one launch
+                (hq_quantized_matmul_swiglu, the reference's
+                dense_hidden_fused), o, down, lm_head: 129 launches
   cpu_baseline  the CPU oracle's MLX-style quantized_matmul on the host cores,
                 on a bounded sample of the same workload (layer 0's seven
                 projections at B)
@@ -199,6 +205,61 @@ def bench_qmm(model, dev, steps):
     return out
 
 
+class FusedPlan:
+    """The decode step with fused launches: per layer q|k|v concatenated
+    along N, o, gate/up with the SwiGLU epilogue, down; then lm_head.
+    Weights are concatenated copies of the Model's (same bytes)."""
+
+    def __init__(self, model, B, dev):
+        import torch
+
+        from higgs_amd import _lib, gen
+
+        self.lib = _lib.lib()
+        self.x = gen.torch_x(1, (B, HIDDEN), dev)
+        self.h = gen.torch_x(2, (B, INTER), dev)
+        self.yq = torch.empty((B, 6144), dtype=torch.bfloat16, device=dev)
+        self.yo = torch.empty((B, HIDDEN), dtype=torch.bfloat16, device=dev)
+        self.yh = torch.empty((B, INTER), dtype=torch.bfloat16, device=dev)
+        self.yl = torch.empty((B, VOCAB), dtype=torch.bfloat16, device=dev)
+        self.keep = []
+        self.plan = []
+        self.bytes = 0
+        for ws in model.layers:
+            qkv = [torch.cat([ws[n][i] for n in ("q", "k", "v")]) for i in range(3)]
+            gu = [torch.cat([ws[n][i] for n in ("gate", "up")]) for i in range(3)]
+            self.keep += [qkv, gu]
+            self.plan.append(("mm", self.yq, self.x, qkv, 6144, HIDDEN))
+            self.plan.append(("mm", self.yo, self.x, ws["o"], HIDDEN, HIDDEN))
+            self.plan.append(("swiglu", self.yh, self.x, gu, INTER, HIDDEN))
+            self.plan.append(("mm", self.yo, self.h, ws["down"], HIDDEN, INTER))
+            self.bytes += (qmv_bytes(B, 6144, HIDDEN) + qmv_bytes(B, HIDDEN, HIDDEN) +
+                           qmv_bytes(B, 2 * INTER, HIDDEN) - 2 * B * INTER +
+                           qmv_bytes(B, HIDDEN, INTER))
+        self.plan.append(("mm", self.yl, self.x, model.lm_head, VOCAB, HIDDEN))
+        self.bytes += qmv_bytes(B, VOCAB, HIDDEN)
+        self.B = B
+        rows = lambda t, n: t.data_ptr() + n * t.stride(0) * t.element_size()
+        self.calls = []
+        for kind, y, x, (w, s, b), N, K in self.plan:
+            if kind == "mm":
+                self.calls.append((0, (y.data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(),
+                                       b.data_ptr(), B, N, K, 1, GROUP, BITS, 2, 2)))
+            else:
+                self.calls.append((1, (y.data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(),
+                                       b.data_ptr(), rows(w, N), rows(s, N), rows(b, N), B, N, K,
+                                       GROUP, BITS, 2, 2)))
+        torch.cuda.synchronize()
+
+    def run(self, stream_ptr):
+        fm, fs = self.lib.hq_quantized_matmul, self.lib.hq_quantized_matmul_swiglu
+        for kind, a in self.calls:
+            rc = (fm if kind == 0 else fs)(*a, stream_ptr)
+            if rc:
+                from higgs_amd import _lib
+                raise _lib.HiggsQmmError(rc, _lib.last_error())
+
+
 def bench_moe(dev, steps):
     """512 tokens, top-8 of 128 experts, hidden 2048, expert
     intermediate 768, 4-bit g64; rows globally sorted by expert, sorted gather_qmm."""
@@ -226,6 +287,23 @@ def bench_moe(dev, steps):
         out[name] = {"rows": T * TK, "experts": E, "N": N, "K": K, "us": round(ms * 1e3, 2),
                      "GB/s": round(byts / (ms * 1e-3) / 1e9, 1)}
         del ws
+    # the whole expert block (qwen3_moe.rs:353-357 around forward_gather_global_sort)
+    blocks = [tuple(gen.torch_quantized(80 + 3 * c + j, *nk, BITS, GROUP, dev, lead=(E,))
+                    for j, nk in enumerate(((I, H), (I, H), (H, I)))) for c in range(3)]
+    x = gen.torch_x(72, (1, T, H), dev)
+    idx_d = torch.from_numpy(idx.astype(np.int32)).to(dev).reshape(1, T, TK)
+    sc = torch.softmax(gen.torch_x(73, (1, T, TK), dev).float(), -1).to(torch.bfloat16)
+
+    def run_block(stream, blocks=blocks):
+        for (g, u, d) in blocks:
+            ops.moe_block(x, idx_d, sc, g, u, d, GROUP, BITS)
+    ms = time_graph(run_block, steps, 1, dev) / len(blocks)
+    byts = used * (3 * (I * H // 2 + 2 * I * (H // GROUP) * 2)) + 2 * T * H * 2 + \
+        T * TK * 2 * (H + I + I + H)
+    out["block"] = {"tokens": T, "top_k": TK, "experts": E, "hidden": H, "intermediate": I,
+                    "launches": 4, "us": round(ms * 1e3, 2),
+                    "GB/s": round(byts / (ms * 1e-3) / 1e9, 1)}
+    del blocks
     torch.cuda.empty_cache()
     return out
 
@@ -346,6 +424,16 @@ def main():
         log(f"[bench] qmm: {extras['qmm']}")
         extras["moe"] = bench_moe(dev, max(3, args.steps // 4))
         log(f"[bench] moe: {extras['moe']}")
+        fp = FusedPlan(model, args.batch, dev)
+        mf = time_graph(fp.run, args.steps, 2, dev)
+        extras["decode_fused"] = {"batch": args.batch, "launches": len(fp.calls),
+                                  "ms_per_step": round(mf, 4),
+                                  "GB/s": round(fp.bytes / (mf * 1e-3) / 1e9, 1),
+                                  "frac": round(fp.bytes / (mf * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "tokens_per_s": round(1e3 / mf, 1)}
+        log(f"[bench] fused decode step: {extras['decode_fused']}")
+        del fp
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
