@@ -788,17 +788,20 @@ hipError_t run_qmvp(const QArgs& a) {
     const int nseg = (int)(a.K / 128);
     const int ntiles = (int)((a.N + 15) / 16);
     // S = 8 segments per round and W <= 8 waves with W * 8 dividing nseg.
-    // When that leaves fewer than 8 waves per tile and tiles are few (small
-    // N), rounds of S = 4 give each tile up to twice the waves. Rounds of
-    // S = 4 also serve x that does not fit LDS when direct x at S = 8 would
-    // spill registers.
+    // Rounds of S = 4 instead (measured on the Llama-3-8B shapes at M = 1):
+    // - when that leaves fewer than 8 waves per tile and tiles are few (small
+    //   N): up to twice the waves per tile, or the same waves in twice the
+    //   rounds (K = 14336: 11.0 against 11.35 us);
+    // - when blocks walk many tiles (the vocabulary projection): 56.8 against
+    //   59.5 us;
+    // - for x that does not fit LDS when direct x at S = 8 would spill.
     auto pick = [&](int S) {
       for (int c = 8; c >= 1; c--)
         if ((nseg / S) % c == 0) return c;
       return 0;
     };
     const int W8 = pick(8), W4 = pick(4);
-    if (W8 < 8 && ntiles <= 512 && W4 > W8)
+    if ((W8 < 8 && ntiles <= 512 && W4 >= W8) || (ntiles >= 16 * device_cus() && W4 == 8))
       return run_qmvp_sd<XDT, SDT, MB, GS, 4, SWI>(a, W4, nseg / (4 * W4));
     if (W8 == 0) return hipErrorNotSupported;
     if (!kDirectOk<MB, GS, 8> && qmvp_lds(a, W8, MB, GS, false, SWI) > 160 * 1024)
