@@ -220,6 +220,19 @@ namespace {
 
 constexpr int GBM = 256, GBN = 256, GBK = 64;
 constexpr int kRD = 3;  // register prefetch depth (K-steps) of the large-tile GEMM
+
+// Tile shapes of the large-tile GEMM: a block computes TN W rows x TM x rows
+// with WAVES waves of WN x WM each. 256 x 256 (8 waves, one block per CU) is
+// the main shape; 128 x 128 (4 waves, two blocks per CU) is for products
+// whose 256-tiles would leave CUs idle (M = 2048 down: 128 tiles for 256
+// CUs).
+template <int SZ> struct GTile;
+template <> struct GTile<256> {
+  static constexpr int TN = 256, TM = 256, WAVES = 8, WN = 128, WM = 64;
+};
+template <> struct GTile<128> {
+  static constexpr int TN = 128, TM = 128, WAVES = 4, WN = 64, WM = 64;
+};
 constexpr int GLD = GBK + 16;  // LDS row stride (elements): 160 B (fewest bank conflicts measured)
 
 struct GKern {
@@ -278,20 +291,24 @@ __device__ __forceinline__ u32x4 deq8(const uint32_t (&wd)[BITS], int qq, float 
   return h;
 }
 
-// SWI: the 256 W rows of a tile are 128 output columns of the gate and the
-// same 128 columns of the up projection, arranged so that a wave's fragments
-// i < 4 are gate rows and i + 4 the matching up rows; the epilogue writes
-// swiglu(gate, up) for 128 columns from registers.
-template <int BITS, int CT, int GS, bool SWI>
-__global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
+// SWI: the TN W rows of a tile are TN/2 output columns of the gate and the
+// same columns of the up projection, arranged so that a wave's fragments
+// i < NI/2 are gate rows and i + NI/2 the matching up rows; the epilogue
+// writes swiglu(gate, up) for TN/2 columns from registers.
+template <int BITS, int CT, int GS, bool SWI, int SZ>
+__global__ __launch_bounds__(GTile<SZ>::WAVES * 64) void qgemm_kernel(GKern a) {
   using T = Mma<CT>;
   using ST = st_t<CT>;
+  using TL = GTile<SZ>;
+  constexpr int GBN = TL::TN, GBM = TL::TM, NT = TL::WAVES * 64;
+  constexpr int NI = TL::WN / 16, NJ = TL::WM / 16;  // fragments per wave in n, m
   extern __shared__ __attribute__((aligned(16))) unsigned char gsm[];
   uint16_t* As = reinterpret_cast<uint16_t*>(gsm);                    // [2][GBN][GLD]  (W)
   uint16_t* Bs = As + 2 * GBN * GLD;                                  // [2][GBM][GLD]  (x)
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wn = wv >> 2, wm = wv & 3;  // wave owns n rows wn*128.., m rows wm*64..
+  // wave owns n rows wn*WN.., m rows wm*WM..
+  const int wn = wv / (GBM / TL::WM), wm = wv % (GBM / TL::WM);
   const int M = a.M, N = a.N, K = a.K;
   // XCD-aware tile order: consecutive block ids go to different XCDs (8 on
   // MI355X), so tile t is given to block id (t % per) * 8 + t / per; each XCD
@@ -310,18 +327,22 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   const int64_t G = K / GS;
   const ST* xg = (const ST*)a.x;
 
-  // x tile (256 x 64): thread copies rows xr + 64j (j < 4), 16-byte chunk xc.
-  // Rows past M read row M-1 (never stored), so every load is unconditional.
+  // x tile (GBM x 64): thread copies rows xr + (NT/8)j (j < 4), 16-byte chunk
+  // xc. Rows past M read row M-1 (never stored), so every load is
+  // unconditional.
   const int xr = tid >> 3, xc = tid & 7;
-  // W tile (256 x 64): thread dequantizes pack wp of row wr.
+  static_assert(GBM == 4 * (NT / 8) && GBN == NT / 2, "thread maps cover the tiles");
+  // W tile (GBN x 64): thread dequantizes pack wp of row wr.
   const int wr = tid >> 1, wp = tid & 1;
   uint32_t xoff[4];  // element offsets into x (the launcher checks M*K < 2^31)
 #pragma unroll
-  for (int j = 0; j < 4; j++) xoff[j] = (uint32_t)min(m0 + xr + 64 * j, M - 1) * (uint32_t)K + xc * 8;
-  // SWI: tile row wr is column n0 + (wr / 128) * 64 + wr % 64 of the gate
-  // (wr % 128 < 64) or of the up projection.
-  const bool w_up = SWI && (wr & 64);
-  const int wn_row = min(SWI ? n0 + (wr >> 7) * 64 + (wr & 63) : n0 + wr, N - 1);
+  for (int j = 0; j < 4; j++)
+    xoff[j] = (uint32_t)min(m0 + xr + (NT / 8) * j, M - 1) * (uint32_t)K + xc * 8;
+  // SWI: tile row wr is column n0 + (wr / WN) * WN/2 + wr % (WN/2) of the gate
+  // (wr % WN < WN/2) or of the up projection.
+  constexpr int HW = TL::WN / 2;
+  const bool w_up = SWI && (wr % TL::WN) >= HW;
+  const int wn_row = min(SWI ? n0 + (wr / TL::WN) * HW + (wr % HW) : n0 + wr, N - 1);
   const uint32_t woff = (uint32_t)((int64_t)wn_row * P) + wp * BITS;
   const uint32_t goff = (uint32_t)((int64_t)wn_row * G);
   const uint32_t* wg = w_up ? a.w2 : a.w;
@@ -344,11 +365,11 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
     *reinterpret_cast<u32x4*>(dst) = deq8<BITS, CT>(p.wd, qq, p.sv, p.bv);
   };
 
-  floatx4 acc[8][4];
+  floatx4 acc[NI][NJ];
 #pragma unroll
-  for (int i = 0; i < 8; i++)
+  for (int i = 0; i < NI; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   // MFMAs of one K-step on LDS buffer `buf`, with the dequantization of the
   // next step's W (registers `wn_`) threaded between them into `buf ^ 1`.
@@ -358,19 +379,19 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
 #pragma unroll
     for (int ks = 0; ks < GBK / 32; ks++) {
       const int kofs = ks * 32 + (lane >> 4) * 8;
-      typename T::frag fb[4];
+      typename T::frag fb[NJ];
 #pragma unroll
-      for (int j = 0; j < 4; j++)
+      for (int j = 0; j < NJ; j++)
         fb[j] = __builtin_bit_cast(typename T::frag, *reinterpret_cast<const u32x4*>(
-                                                         bs + (wm * 64 + j * 16 + (lane & 15)) * GLD + kofs));
+                                                         bs + (wm * TL::WM + j * 16 + (lane & 15)) * GLD + kofs));
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < NI; i++) {
         const typename T::frag fa = __builtin_bit_cast(
             typename T::frag,
-            *reinterpret_cast<const u32x4*>(as + (wn * 128 + i * 16 + (lane & 15)) * GLD + kofs));
+            *reinterpret_cast<const u32x4*>(as + (wn * TL::WN + i * 16 + (lane & 15)) * GLD + kofs));
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = T::mma(fa, fb[j], acc[i][j]);
-        if ((i & 3) == 0) wchunk(wn_, buf ^ 1, ks * 2 + (i >> 2));
+        for (int j = 0; j < NJ; j++) acc[i][j] = T::mma(fa, fb[j], acc[i][j]);
+        if (i % (NI / 2) == 0) wchunk(wn_, buf ^ 1, ks * 2 + i / (NI / 2));
       }
     }
   };
@@ -391,7 +412,7 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
     uint16_t* bs = Bs + buf * GBM * GLD;
 #pragma unroll
     for (int j = 0; j < 4; j++)
-      *reinterpret_cast<u32x4*>(bs + (xr + 64 * j) * GLD + xc * 8) = d[j];
+      *reinterpret_cast<u32x4*>(bs + (xr + (NT / 8) * j) * GLD + xc * 8) = d[j];
   };
 #pragma unroll
   for (int d = 0; d < kRD; d++) {
@@ -418,22 +439,22 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
     }
   }
 
-  // epilogue: acc[i][j][v] = y[m][n], n = n0 + wn*128 + i*16 + 4*(lane>>4) + v,
-  // m = m0 + wm*64 + j*16 + (lane & 15)
+  // epilogue: acc[i][j][v] = y[m][n], n = n0 + wn*WN + i*16 + 4*(lane>>4) + v,
+  // m = m0 + wm*WM + j*16 + (lane & 15)
   ST* yg = (ST*)a.y;
   if constexpr (SWI) {
-    // acc[i] gate and acc[i + 4] up of column n0 + wn*64 + i*16 + 4*(lane>>4) + v
+    // acc[i] gate and acc[i + NI/2] up of column n0 + wn*WN/2 + i*16 + 4*(lane>>4) + v
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int n = n0 + wn * 64 + i * 16 + 4 * (lane >> 4);
+    for (int i = 0; i < NI / 2; i++) {
+      const int n = n0 + wn * HW + i * 16 + 4 * (lane >> 4);
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int m = m0 + wm * 64 + j * 16 + (lane & 15);
+      for (int j = 0; j < NJ; j++) {
+        const int m = m0 + wm * TL::WM + j * 16 + (lane & 15);
         if (m >= M) continue;
         float h[4];
 #pragma unroll
         for (int v = 0; v < 4; v++)
-          h[v] = swiglu_f32(DT_<CT>::round(acc[i][j][v]), DT_<CT>::round(acc[i + 4][j][v]));
+          h[v] = swiglu_f32(DT_<CT>::round(acc[i][j][v]), DT_<CT>::round(acc[i + NI / 2][j][v]));
         if (n + 3 < N) {
           u32x2 o;
           o[0] = pack2<CT>(h[0], h[1]);
@@ -449,11 +470,11 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
     return;
   }
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int n = n0 + wn * 128 + i * 16 + 4 * (lane >> 4);
+  for (int i = 0; i < NI; i++) {
+    const int n = n0 + wn * TL::WN + i * 16 + 4 * (lane >> 4);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int m = m0 + wm * 64 + j * 16 + (lane & 15);
+    for (int j = 0; j < NJ; j++) {
+      const int m = m0 + wm * TL::WM + j * 16 + (lane & 15);
       if (m >= M) continue;
       if (n + 3 < N) {
         u32x2 o;
@@ -469,14 +490,28 @@ __global__ __launch_bounds__(512, 1) void qgemm_kernel(GKern a) {
   }
 }
 
-template <int CT, int GS, bool SWI>
-hipError_t run_qgemm(const QArgs& a) {
+int gemm_device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      cus = v;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+template <int CT, int GS, bool SWI, int SZ>
+hipError_t run_qgemm_sz(const QArgs& a) {
+  using TL = GTile<SZ>;
   GKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
   k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
-  auto fn = qgemm_kernel<HQ_BITS, CT, GS, SWI>;
-  const size_t lds = (size_t)2 * (GBN + GBM) * GLD * 2;
+  auto fn = qgemm_kernel<HQ_BITS, CT, GS, SWI, SZ>;
+  const size_t lds = (size_t)2 * (TL::TN + TL::TM) * GLD * 2;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -484,10 +519,19 @@ hipError_t run_qgemm(const QArgs& a) {
     if (e != hipSuccess) return e;
     attr = true;
   }
-  const int ont = SWI ? GBN / 2 : GBN;
-  const unsigned ntiles = (unsigned)(((a.N + ont - 1) / ont) * ((a.M + GBM - 1) / GBM));
-  hipLaunchKernelGGL(fn, dim3(ntiles), dim3(512), lds, a.stream, k);
+  const int ont = SWI ? TL::TN / 2 : TL::TN;
+  const unsigned ntiles = (unsigned)(((a.N + ont - 1) / ont) * ((a.M + TL::TM - 1) / TL::TM));
+  hipLaunchKernelGGL(fn, dim3(ntiles), dim3(TL::WAVES * 64), lds, a.stream, k);
   return hipGetLastError();
+}
+
+// 256-tiles unless they would leave CUs idle; then 128-tiles (4x the tiles).
+template <int CT, int GS, bool SWI>
+hipError_t run_qgemm(const QArgs& a) {
+  const int64_t ont = SWI ? 128 : 256;
+  const int64_t t256 = ((a.N + ont - 1) / ont) * ((a.M + 255) / 256);
+  if (t256 < gemm_device_cus()) return run_qgemm_sz<CT, GS, SWI, 128>(a);
+  return run_qgemm_sz<CT, GS, SWI, 256>(a);
 }
 
 template <int CT, bool SWI = false>
