@@ -24,6 +24,9 @@ Printed JSON line (one, on stdout):
   moe           configs[4]: sorted gather_qmm (gate, down) at the MoE shapes,
                 and the whole expert block on device (sort, fused gate/up +
                 SwiGLU, down, unsort + score-weighted combine)
+  configs       configs[0] (Llama-3.2-1B up-proj qmv at B=1) and configs[3]
+                (Qwen3-1.7B gate/up and down at bits 2/3/8 g64 and 4-bit
+                g32/g128, B=1 GB/s and M=512 TFLOP/s)
   decode_fused  the same decode step with the launches fused: q|k|v
                 concatenated (one launch), gate/up + SwiGLU in one launch
                 (hq_quantized_matmul_swiglu, the reference's
@@ -308,6 +311,47 @@ def bench_moe(dev, steps):
     return out
 
 
+def bench_configs(dev, steps):
+    """per-launch time over distinct weight copies
+    (about 2 GB of distinct copies: 8x the 256 MB Infinity Cache)."""
+    import torch
+
+    from higgs_amd import _lib, gen
+
+    lib = _lib.lib()
+    out = {}
+
+    def one(M, N, K, bits, g, tag):
+        wb = N * K * bits // 8 + 2 * N * (K // g) * 2
+        copies = max(2, min(256, (1 << 31) // wb + 1))
+        ws = [gen.torch_quantized(500 + c, N, K, bits, g, dev,
+                                  bias_noise=(1e-3 if tag == "c0" else 0.0)) for c in range(copies)]
+        x = gen.torch_x(501, (M, K), dev)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+        def run(stream, ws=ws):
+            for (w, s, b) in ws:
+                _lib.check(lib.hq_quantized_matmul(y.data_ptr(), x.data_ptr(), w.data_ptr(),
+                                                   s.data_ptr(), b.data_ptr(), M, N, K, 1, g,
+                                                   bits, 2, 2, stream))
+        ms = time_graph(run, steps, 1, dev) / len(ws)
+        r = {"M": M, "N": N, "K": K, "bits": bits, "group_size": g, "us": round(ms * 1e3, 3)}
+        if M <= 8:
+            r["GB/s"] = round(qmv_bytes(M, N, K, bits, g) / (ms * 1e-3) / 1e9, 1)
+        else:
+            r["tflops"] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)
+        del ws
+        return r
+
+    out["c0_llama32_1b_up"] = one(1, 8192, 2048, 4, 64, "c0")
+    for bits, g in ((2, 64), (3, 64), (8, 64), (4, 32), (4, 128)):
+        for M in (1, 512):
+            for name, N, K in (("gate_up", 6144, 2048), ("down", 2048, 6144)):
+                out[f"c3_{bits}b_g{g}_M{M}_{name}"] = one(M, N, K, bits, g, "c3")
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(model, B, target_s):
     """Oracle quantized_matmul (MLX-CPU-style restatement, oracle/hq_oracle.c
     hqo_qmm_mlx) on the host, over layer 0's seven projections at batch B."""
@@ -424,6 +468,8 @@ def main():
         log(f"[bench] qmm: {extras['qmm']}")
         extras["moe"] = bench_moe(dev, max(3, args.steps // 4))
         log(f"[bench] moe: {extras['moe']}")
+        extras["configs"] = bench_configs(dev, max(3, args.steps // 4))
+        log(f"[bench] configs: {extras['configs']}")
         fp = FusedPlan(model, args.batch, dev)
         mf = time_graph(fp.run, args.steps, 2, dev)
         extras["decode_fused"] = {"batch": args.batch, "launches": len(fp.calls),

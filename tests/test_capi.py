@@ -154,3 +154,59 @@ def test_prefix_broadcast_rule():
     assert pb((1,), (7,)) and pb((), (7,))
     assert not pb((3,), (2, 3))          # x broadcast along a leading dim
     assert not pb((1, 3), (2, 3))
+
+
+# --- fused SwiGLU and MoE entry points: validation before any launch ---------
+
+def swiglu_mm(**kw):
+    a = dict(h=FAKE, x=FAKE, wg=FAKE, sg=FAKE, bg=FAKE, wu=FAKE, su=FAKE, bu=FAKE, M=1, N=64,
+             K=1024, g=64, bits=4, xdt=2, sdt=2)
+    a.update(kw)
+    return _lib.lib().hq_quantized_matmul_swiglu(
+        a["h"], a["x"], a["wg"], a["sg"], a["bg"], a["wu"], a["su"], a["bu"], a["M"], a["N"],
+        a["K"], a["g"], a["bits"], a["xdt"], a["sdt"], None)
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(bits=7), 1, "bits 7 is not supported"),
+    (dict(K=96), 1, "divisible by the group size"),
+    (dict(wu=0), 1, "NULL"),
+    (dict(h=FAKE + 4), 1, "16-byte aligned"),
+    (dict(xdt=0, sdt=0), 2, "one 16-bit dtype"),
+    (dict(xdt=2, sdt=1), 2, "one 16-bit dtype"),
+    (dict(M=3, K=768), 2, "K % 1024 == 0"),
+    (dict(M=300, K=97 * 32, g=32), 2, "K % 64 == 0"),
+])
+def test_quantized_matmul_swiglu_rejects(kw, code, needle):
+    assert swiglu_mm(**kw) == code
+    assert needle in _lib.last_error()
+
+
+def test_swiglu_entry_empty_and_shape_errors():
+    assert swiglu_mm(M=0) == 0 and swiglu_mm(N=0) == 0
+    L = _lib.lib()
+    assert L.hq_swiglu(FAKE, FAKE, FAKE, 0, 2, None) == 0
+    assert L.hq_swiglu(FAKE, FAKE, FAKE, 16, 5, None) == 1 and "floating" in _lib.last_error()
+    assert L.hq_swiglu(FAKE, FAKE, FAKE, -1, 2, None) == 1
+    assert L.hq_gather_qmm_swiglu(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, 4,
+                                  4, 2, 1, 64, 128, 64, 4, 2, 2, None) == 1
+    assert "rhs_indices" in _lib.last_error()
+    assert L.hq_gather_qmm_swiglu(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 6,
+                                  4, 2, 1, 64, 128, 64, 4, 2, 2, None) == 1
+    assert "multiple of x's batch" in _lib.last_error()
+
+
+def test_moe_sort_and_combine_reject():
+    L = _lib.lib()
+    assert L.hq_moe_sort(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 8, 128, None) == 0
+    assert L.hq_moe_sort(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 8, 4096, None) == 1
+    assert "num_experts <= 2048" in _lib.last_error()
+    assert L.hq_moe_sort(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 0, 128, None) == 1
+    assert L.hq_moe_sort(FAKE, FAKE, FAKE, FAKE, None, 64, 8, 128, None) == 1
+    assert "idx" in _lib.last_error()
+    assert L.hq_moe_combine(FAKE, FAKE, FAKE, FAKE, 0, 8, 2048, 2, 2, None) == 0
+    assert L.hq_moe_combine(FAKE, FAKE, FAKE, FAKE, 4, 8, 2048, 9, 2, None) == 1
+    assert L.hq_moe_combine(FAKE, FAKE, None, FAKE, 4, 8, 2048, 2, 2, None) == 1
+    assert "NULL" in _lib.last_error()
+    assert L.hq_moe_combine(FAKE + 2, FAKE, FAKE, FAKE, 4, 8, 2048, 2, 2, None) == 1
+    assert "aligned" in _lib.last_error()
