@@ -233,6 +233,9 @@ template <> struct GTile<256> {
 template <> struct GTile<128> {
   static constexpr int TN = 128, TM = 128, WAVES = 4, WN = 64, WM = 64;
 };
+template <> struct GTile<64> {
+  static constexpr int TN = 64, TM = 64, WAVES = 2, WN = 32, WM = 64;
+};
 constexpr int GLD = GBK + 16;  // LDS row stride (elements): 160 B (fewest bank conflicts measured)
 
 struct GKern {
@@ -525,13 +528,18 @@ hipError_t run_qgemm_sz(const QArgs& a) {
   return hipGetLastError();
 }
 
-// 256-tiles unless they would leave CUs idle; then 128-tiles (4x the tiles).
+// The largest tile that still gives every CU a tile: 256, else 128, else
+// 64 (each step down has 4x the tiles and less reuse per LDS byte).
 template <int CT, int GS, bool SWI>
 hipError_t run_qgemm(const QArgs& a) {
-  const int64_t ont = SWI ? 128 : 256;
-  const int64_t t256 = ((a.N + ont - 1) / ont) * ((a.M + 255) / 256);
-  if (t256 < gemm_device_cus()) return run_qgemm_sz<CT, GS, SWI, 128>(a);
-  return run_qgemm_sz<CT, GS, SWI, 256>(a);
+  const int cus = gemm_device_cus();
+  auto tiles = [&](int64_t t) {
+    const int64_t ont = SWI ? t / 2 : t;
+    return ((a.N + ont - 1) / ont) * ((a.M + t - 1) / t);
+  };
+  if (tiles(256) >= cus) return run_qgemm_sz<CT, GS, SWI, 256>(a);
+  if (tiles(128) >= cus) return run_qgemm_sz<CT, GS, SWI, 128>(a);
+  return run_qgemm_sz<CT, GS, SWI, 64>(a);
 }
 
 template <int CT, bool SWI = false>
