@@ -674,6 +674,292 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming decode GEMV for one row of x (M == 1) with x and scales of one
+// 16-bit type: the common decode case.
+//
+// A row tile is 16 output columns. Each of a block's W waves owns a fixed K
+// range of every tile: RW rounds of S segments (128 elements each), so
+// K = W * RW * S * 128. A wave's work is a sequence of items (tile, round)
+// over the tiles t = blockIdx.x, blockIdx.x + gridDim.x, ... . The first
+// items' weight loads go out right after this wave's x loads, and each wave
+// stages only its own K range of x, so the first MFMA waits for no other
+// wave.
+// With RING == 3 (blocks that walk several tiles) the loads of item i + 2 are
+// issued before item i is computed (three register buffers); with RING == 1
+// (one item per wave) there is one buffer and fewer registers, so more blocks
+// are resident at once. x is staged in LDS in the MFMA pair order;
+// the group sums X come from one MFMA per k-step against an all-ones operand,
+// so staging does no arithmetic. With W > 1 the partial sums of a tile meet
+// in LDS after one barrier (double-buffered slots, fixed order); with W == 1
+// a wave finishes its tiles alone.
+//
+// SWI (fused gate/up + SwiGLU): a tile's gate rounds run first, then its up
+// rounds; the gate sum of each column waits in a register of the lane that
+// writes the column.
+// ---------------------------------------------------------------------------
+struct SKern {
+  void* y;
+  const void* x;
+  const uint32_t* w;
+  const void* s;
+  const void* b;
+  const uint32_t* w2;  // SwiGLU up projection (gate is w/s/b)
+  const void* s2;
+  const void* b2;
+  int N, K;
+  int ntiles;   // ceil(N / 16)
+  int RW;       // rounds per wave per tile
+  uint32_t nib_mask, off_pair;
+};
+
+template <int BITS, int XDT, int GS, int S, int RING, bool SPLIT, bool SWI>
+__global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
+  constexpr int Z = 128 / GS;                        // groups per segment
+  constexpr int SU = (16 / Z) < S ? 16 / Z : S;      // segments per accumulator
+  constexpr int NB = S / SU;                         // accumulators per round
+  constexpr int NSLOT = SU * Z;                      // (segment, group) slots used
+  static_assert(SU % 2 == 0 && S % SU == 0, "segments pair up into two MFMA chains");
+  static_assert(RING == 1 || RING == 3, "one or three register buffers");
+  using T = XMma<XDT>;
+  using XS = st_t<XDT>;
+  using frag = typename T::frag;
+  constexpr float OFF = kExact8<BITS, XDT> ? 0.f : T::OFF;
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int W = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int N = a.N, K = a.K, RW = a.RW;
+  const int64_t P = (int64_t)(K >> 5) * BITS;  // words per weight row
+  const int G = K / GS;                        // groups per row
+  // LDS: x [K] in pair order | 64 B of zeros | red [2][W][16] floats
+  const int zoff = K * 2;
+  float* red = reinterpret_cast<float*>(smem + zoff + 64);
+
+  const int nl = lane & 15, q = lane >> 4;
+  // A side: A row nl is slot nl = (segment uA of the accumulator, group hA);
+  // the lane feeds k-block q of that segment when the block lies in group hA.
+  const int uA = nl / Z, hA = nl % Z;
+  const bool validA = (hA == q * Z / 4) && (nl < NSLOT);
+  // D side: value v of this lane is slot 4q + v; its group is g0 + v.
+  const int gsig = (4 * q < NSLOT) ? 4 * q : 0;
+  float keep[4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) keep[v] = (4 * q + v < NSLOT) ? 1.f : 0.f;
+
+  const uint32_t mask_s = a.nib_mask;
+  uint32_t off_v;
+  asm("v_mov_b32 %0, %1" : "=v"(off_v) : "s"(a.off_pair));
+
+  struct Item {
+    uint32_t wd[S][BITS];
+    u32x2 sv[NB], bv[NB];  // 4 consecutive 16-bit scales / biases per accumulator
+  };
+  const int RT = SWI ? 2 * RW : RW;  // items per tile
+  const int step = gridDim.x;
+
+  // item (tile t, index j): half hf = j / RW (SwiGLU), round j % RW
+  auto issue = [&](Item& r, int t, int j) {
+    const int hf = SWI ? (j >= RW ? 1 : 0) : 0;
+    const int rnd = j - hf * RW;
+    const int n = min(t * 16 + nl, N - 1);
+    const int seg_base = (wv * RW + rnd) * S;
+    const uint32_t* wp = (hf ? a.w2 : a.w) + (int64_t)n * P + (int64_t)(seg_base * 4 + q) * BITS;
+#pragma unroll
+    for (int u = 0; u < S; u++) load_pack<BITS>(wp + u * 4 * BITS, r.wd[u]);
+    const XS* sp = (const XS*)(hf ? a.s2 : a.s) + (int64_t)n * G + seg_base * Z + gsig;
+    const XS* bp = (const XS*)(hf ? a.b2 : a.b) + (int64_t)n * G + seg_base * Z + gsig;
+#pragma unroll
+    for (int jb = 0; jb < NB; jb++) {
+      r.sv[jb] = *reinterpret_cast<const u32x2*>(sp + jb * NSLOT);
+      r.bv[jb] = *reinterpret_cast<const u32x2*>(bp + jb * NSLOT);
+    }
+  };
+  auto advance = [&](int& t, int& j) {
+    if (++j == RT) { j = 0; t += step; }
+  };
+
+  // ---- x of this wave's K range (the only x it reads), the first items'
+  // weight loads, then x into LDS in pair order. Waves stage their own range,
+  // so no block barrier precedes the first MFMA.
+  const XS* xg = (const XS*)a.x + (int64_t)wv * RW * S * 128;
+  unsigned char* xl = smem + wv * RW * S * 256;
+  const int xch = RW * S * 16;  // 16-byte chunks in the range
+  constexpr int XPRE = 2;  // chunks per lane loaded ahead of the weights
+  u32x4 xr[XPRE];
+#pragma unroll
+  for (int c = 0; c < XPRE; c++)
+    xr[c] = (lane + 64 * c < xch) ? *reinterpret_cast<const u32x4*>(xg + (lane + 64 * c) * 8)
+                                  : u32x4{0u, 0u, 0u, 0u};
+  Item r0, r1, r2;
+  int ti = blockIdx.x, ji = 0;  // next item to issue
+  if (ti < a.ntiles) issue(r0, ti, ji);
+  advance(ti, ji);
+  if constexpr (RING == 3) {
+    if (ti < a.ntiles) issue(r1, ti, ji);
+    advance(ti, ji);
+  }
+  auto xstore = [&](int c, const u32x4 d) {
+    u32x4 o;
+    o[0] = (d[0] & 0xffffu) | (d[2] << 16);
+    o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
+    o[2] = (d[1] & 0xffffu) | (d[3] << 16);
+    o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
+    *reinterpret_cast<u32x4*>(xl + c * 16) = o;
+  };
+#pragma unroll
+  for (int c = 0; c < XPRE; c++)
+    if (lane + 64 * c < xch) xstore(lane + 64 * c, xr[c]);
+  for (int c = lane + 64 * XPRE; c < xch; c += 64)
+    xstore(c, *reinterpret_cast<const u32x4*>(xg + c * 8));
+  if (lane < 4) reinterpret_cast<u32x4*>(smem + zoff)[lane] = u32x4{0u, 0u, 0u, 0u};
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  constexpr uint32_t ONE2 = XDT == DT_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
+
+  auto compute = [&](const Item& r, int j) {
+    const int hf = SWI ? (j >= RW ? 1 : 0) : 0;
+    const int rnd = j - hf * RW;
+    const int seg_base = (wv * RW + rnd) * S;
+#pragma unroll
+    for (int jb = 0; jb < NB; jb++) {
+      const int real = validA ? (seg_base + jb * SU + uA) * 256 + q * 64 : zoff;
+      // two accumulator chains (even / odd segments) so consecutive MFMAs do
+      // not wait for each other; segments are unpacked two at a time into
+      // separate registers
+      floatx4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+      floatx4 X = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int uu = 0; uu < SU; uu += 2) {
+        u32x4 av[2][4], bw[2][4];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+          const int addr = (uA == uu + e) ? real : zoff;
+#pragma unroll
+          for (int i = 0; i < 4; i++) av[e][i] = *reinterpret_cast<const u32x4*>(smem + addr + i * 16);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            if constexpr (BITS == 4) {
+              const uint32_t w = r.wd[jb * SU + uu + e][i];
+              bw[e][i][0] = (w & mask_s) | off_v;
+              bw[e][i][1] = ((w >> 4) & mask_s) | off_v;
+              bw[e][i][2] = ((w >> 8) & mask_s) | off_v;
+              bw[e][i][3] = ((w >> 12) & mask_s) | off_v;
+            } else {
+              bw[e][i] = unpack_step<BITS, XDT>(r.wd[jb * SU + uu + e], i);
+            }
+          }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          d0 = T::mma(__builtin_bit_cast(frag, av[0][i]), __builtin_bit_cast(frag, bw[0][i]), d0);
+          d1 = T::mma(__builtin_bit_cast(frag, av[1][i]), __builtin_bit_cast(frag, bw[1][i]), d1);
+        }
+      }
+      // group sums: the lane's own x (or zeros) times ones
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const u32x4 xa = *reinterpret_cast<const u32x4*>(smem + real + i * 16);
+        X = T::mma(__builtin_bit_cast(frag, xa), __builtin_bit_cast(frag, ones), X);
+      }
+      const u32x2 sp = r.sv[jb], bp = r.bv[jb];
+      float sv[4], bv[4];
+      sv[0] = DT_<XDT>::to_f32((uint16_t)(sp[0] & 0xffffu));
+      sv[1] = DT_<XDT>::to_f32((uint16_t)(sp[0] >> 16));
+      sv[2] = DT_<XDT>::to_f32((uint16_t)(sp[1] & 0xffffu));
+      sv[3] = DT_<XDT>::to_f32((uint16_t)(sp[1] >> 16));
+      bv[0] = DT_<XDT>::to_f32((uint16_t)(bp[0] & 0xffffu));
+      bv[1] = DT_<XDT>::to_f32((uint16_t)(bp[0] >> 16));
+      bv[2] = DT_<XDT>::to_f32((uint16_t)(bp[1] & 0xffffu));
+      bv[3] = DT_<XDT>::to_f32((uint16_t)(bp[1] >> 16));
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const float bo = fmaf(-OFF, sv[v], bv[v]);
+        acc[v] = fmaf(sv[v], d0[v] + d1[v], fmaf(bo, X[v], acc[v]));
+      }
+    }
+  };
+
+  float gate = 0.f;  // SWI: gate sum of column t*16 + nl (wave 0, q == 0)
+  int buf = 0;
+  // This wave's partial for the 16 columns of the tile, summed over the
+  // block: the total lands in lanes q == 0 of wave 0.
+  auto reduce_tile = [&]() -> float {
+    float part = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      part = fmaf(keep[v], acc[v], part);
+      acc[v] = 0.f;
+    }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    if constexpr (SPLIT) {
+      float* rb = red + buf * (W * 16);
+      if (q == 0) rb[wv * 16 + nl] = part;
+      __syncthreads();
+      buf ^= 1;
+      float sum = 0.f;
+      if (wv == 0)
+        for (int w2 = 0; w2 < W; w2++) sum += rb[w2 * 16 + nl];
+      return sum;
+    } else {
+      return part;
+    }
+  };
+  auto finish = [&](int t, int j) {
+    const float sum = reduce_tile();
+    if constexpr (SWI) {
+      if (j == RW - 1) {
+        gate = sum;
+        return;
+      }
+    }
+    if (wv == 0 && q == 0 && t * 16 + nl < N) {
+      using OS = st_t<XDT>;
+      float o = sum;
+      if constexpr (SWI) o = swiglu_f32(DT_<XDT>::round(gate), DT_<XDT>::round(sum));
+      ((OS*)a.y)[t * 16 + nl] = DT_<XDT>::from_f32(o);
+    }
+  };
+
+  int tc = blockIdx.x, jc = 0;  // next item to compute
+  if constexpr (RING == 1) {
+    while (tc < a.ntiles) {
+      compute(r0, jc);
+      if (jc == RW - 1 || jc == RT - 1) finish(tc, jc);
+      advance(tc, jc);
+      if (tc >= a.ntiles) break;
+      if (ti < a.ntiles) issue(r0, ti, ji);
+      advance(ti, ji);
+    }
+  } else {
+    // items in order over three buffers; the loop body is unrolled by three
+    // so every buffer index is a compile-time constant
+    while (tc < a.ntiles) {
+      if (ti < a.ntiles) issue(r2, ti, ji);
+      advance(ti, ji);
+      compute(r0, jc);
+      if (jc == RW - 1 || jc == RT - 1) finish(tc, jc);
+      advance(tc, jc);
+      if (tc >= a.ntiles) break;
+      if (ti < a.ntiles) issue(r0, ti, ji);
+      advance(ti, ji);
+      compute(r1, jc);
+      if (jc == RW - 1 || jc == RT - 1) finish(tc, jc);
+      advance(tc, jc);
+      if (tc >= a.ntiles) break;
+      if (ti < a.ntiles) issue(r1, ti, ji);
+      advance(ti, ji);
+      compute(r2, jc);
+      if (jc == RW - 1 || jc == RT - 1) finish(tc, jc);
+      advance(tc, jc);
+    }
+  }
+}
+
 int device_cus() {
   static int cus = 0;
   if (cus == 0) {
@@ -685,6 +971,44 @@ int device_cus() {
       cus = 256;
   }
   return cus;
+}
+
+// Launches the streaming M == 1 kernel: W waves per block, RW rounds of S
+// segments per wave per tile (K == W * RW * S * 128), `grid` blocks; RING 3
+// when blocks walk more than one tile.
+template <int XDT, int GS, int S, bool SWI>
+hipError_t run_qmvs(const QArgs& a, int W, int RW, int grid) {
+  if (a.K != (int64_t)W * RW * S * 128 || W < 1 || W > 8) return hipErrorNotSupported;
+  const size_t lds = (size_t)a.K * 2 + 64 + (size_t)2 * W * 16 * 4;
+  if (lds > 160 * 1024) return hipErrorNotSupported;
+  SKern k;
+  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
+  k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
+  k.N = (int)a.N; k.K = (int)a.K; k.RW = RW;
+  k.ntiles = (int)((a.N + 15) / 16);
+  k.nib_mask = 0x000F000Fu;
+  k.off_pair = XMma<XDT>::OFFB;
+  if (grid > k.ntiles) grid = k.ntiles;
+  if (grid < 1) grid = 1;
+  const bool ring = grid < k.ntiles || RW > 1 || SWI;
+  const int which = (ring ? 2 : 0) + (W > 1 ? 1 : 0);
+  using Fn = void (*)(SKern);
+  static const Fn fns[4] = {qmvs_kernel<HQ_BITS, XDT, GS, S, 1, false, SWI>,
+                            qmvs_kernel<HQ_BITS, XDT, GS, S, 1, true, SWI>,
+                            qmvs_kernel<HQ_BITS, XDT, GS, S, 3, false, SWI>,
+                            qmvs_kernel<HQ_BITS, XDT, GS, S, 3, true, SWI>};
+  const Fn fn = fns[which];
+  if (lds > 64 * 1024) {
+    static bool big[4] = {false, false, false, false};
+    if (!big[which]) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      if (e != hipSuccess) return e;
+      big[which] = true;
+    }
+  }
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, a.stream, k);
+  return hipGetLastError();
 }
 
 // Bytes of LDS one block of the persistent kernel uses.
@@ -845,14 +1169,40 @@ hipError_t run_qmvx(const QArgs& a) {
   return hipGetLastError();
 }
 
+// One x row, x and scales of one 16-bit type, K % 1024 == 0, many tiles (a
+// vocabulary-sized projection): the streaming kernel with one block per tile
+// and rounds of 8 segments over K / 1024 waves. Measured at 128256 x 4096
+// (M = 1, 4-bit g64): 52.5 us (5.6 TB/s) against 58-67 us for the persistent
+// kernel below. On the smaller Llama-3-8B and Qwen3 shapes the two kernels
+// measured within a few percent of each other (faster or slower by shape),
+// and the persistent kernel keeps them.
+template <int XDT, int GS, bool SWI>
+hipError_t run_qmvs_auto(const QArgs& a) {
+  if constexpr (SWI) {
+    return hipErrorNotSupported;
+  } else {
+    const int ntiles = (int)((a.N + 15) / 16);
+    const int n8 = (int)(a.K / 1024);
+    if (a.K % 1024 != 0 || n8 < 2 || n8 > 8 || ntiles < 2048) return hipErrorNotSupported;
+    return run_qmvs<XDT, GS, 8, false>(a, n8, 1, ntiles);
+  }
+}
+
 template <int XDT, int SDT, int MB, int GS, bool SWI>
 hipError_t run_qmvx_any(const QArgs& a) {
+  const bool single = a.batch == 1 && !a.lhs && !a.rhs;
+  if constexpr (MB == 1 && XDT == SDT) {
+    if (single) {
+      hipError_t e = run_qmvs_auto<XDT, GS, SWI>(a);
+      if (e != hipErrorNotSupported) return e;
+    }
+  }
   if constexpr (SWI) {
-    // fused SwiGLU: persistent kernel only (batch 1, K % 1024 == 0)
-    if (a.batch != 1 || a.lhs || a.rhs) return hipErrorNotSupported;
+    // fused SwiGLU: persistent kernels only (batch 1, K % 1024 == 0)
+    if (!single) return hipErrorNotSupported;
     return run_qmvp<XDT, SDT, MB, GS, true>(a);
   } else {
-    if (a.batch == 1 && !a.lhs && !a.rhs) {
+    if (single) {
       hipError_t e = run_qmvp<XDT, SDT, MB, GS, false>(a);
       if (e != hipErrorNotSupported) return e;
     }

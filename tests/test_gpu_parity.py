@@ -293,3 +293,30 @@ def test_c3_qwen3_bit_group_sweep(dev, bits, g, M):
     for N, K in ((6144, 2048), (2048, 6144)):
         _sampled_rows_check(dev, M, N, K, bits, g, seed=bits * 100 + g + M, n_rows=128,
                             bias_noise=0.0)
+
+
+# --- vocabulary-sized single-row products (the streaming decode kernel) ------
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("bits,g", [(4, 64), (4, 32), (4, 128), (2, 64), (3, 64), (8, 64)])
+@pytest.mark.parametrize("K", [2048, 8192])
+def test_wide_single_row(dev, dt, bits, g, K):
+    """M = 1 with >= 2048 row tiles (N = 32771: the last tile is partial) takes
+    the one-block-per-tile streaming kernel; sampled rows against the oracle."""
+    tdt, odt = (torch.bfloat16, O.BF16) if dt == "bf16" else (torch.float16, O.F16)
+    N = 32771
+    seed = 7000 + K + 10 * bits + g
+    W, S, B = gen.torch_quantized(seed, N, K, bits, g, dev, dtype=tdt)
+    X = gen.torch_x(seed + 1, (1, K), dev, dtype=tdt)
+    Y = ops.quantized_matmul(X, W, S, B, True, g, bits)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([[0, N - 16, N - 1], rng.integers(0, N, 256)]))
+    rt = torch.from_numpy(rows).to(dev)
+    w = W[rt].cpu().numpy().view(np.uint32)
+    s = S[rt].cpu().view(torch.int16).numpy().view(np.uint16)
+    b = B[rt].cpu().view(torch.int16).numpy().view(np.uint16)
+    x = X.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = O.qmm_f64(x, odt, w, s, b, odt, g, bits)
+    err = rel_err(to_host_f64(Y[:, rt]), ref)
+    assert err <= TOL[odt], (N, K, bits, g, dt, err)
