@@ -676,27 +676,21 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
 
 // ---------------------------------------------------------------------------
 // Streaming decode GEMV for one row of x (M == 1) with x and scales of one
-// 16-bit type: the common decode case.
+// 16-bit type: the decode case.
 //
-// A row tile is 16 output columns. Each of a block's W waves owns a fixed K
-// range of every tile: RW rounds of S segments (128 elements each), so
-// K = W * RW * S * 128. A wave's work is a sequence of items (tile, round)
-// over the tiles t = blockIdx.x, blockIdx.x + gridDim.x, ... . The first
-// items' weight loads go out right after this wave's x loads, and each wave
-// stages only its own K range of x, so the first MFMA waits for no other
-// wave.
-// With RING == 3 (blocks that walk several tiles) the loads of item i + 2 are
-// issued before item i is computed (three register buffers); with RING == 1
-// (one item per wave) there is one buffer and fewer registers, so more blocks
-// are resident at once. x is staged in LDS in the MFMA pair order;
-// the group sums X come from one MFMA per k-step against an all-ones operand,
-// so staging does no arithmetic. With W > 1 the partial sums of a tile meet
-// in LDS after one barrier (double-buffered slots, fixed order); with W == 1
-// a wave finishes its tiles alone.
-//
-// SWI (fused gate/up + SwiGLU): a tile's gate rounds run first, then its up
-// rounds; the gate sum of each column waits in a register of the lane that
-// writes the column.
+// A row tile is 16 output columns; a block takes TPB consecutive tiles. Each
+// of its W waves owns RW 8-segment (1024-element) K ranges of every tile, so
+// K = W * RW * 1024; an item is one (tile, half, range), where the half is the
+// gate or the up projection of the fused SwiGLU (SWI) and there is one half
+// otherwise. A wave loads its x ranges, issues the weight and scale loads of
+// all its items, stages its x in LDS in the MFMA pair order (waves stage only
+// what they read, so no block barrier precedes the first MFMA), then computes
+// the items in order. The group sums X of x come from
+// one MFMA per k-step against an all-ones operand, so staging does no
+// arithmetic. With W > 1 the partial sums of a tile meet in LDS after one
+// barrier (double-buffered slots, fixed order). Loads of a tile past the last
+// one read the last tile again (never computed): the issue code stays
+// straight, so waiting for one tile's loads does not wait for the next's.
 // ---------------------------------------------------------------------------
 struct SKern {
   void* y;
@@ -704,23 +698,24 @@ struct SKern {
   const uint32_t* w;
   const void* s;
   const void* b;
-  const uint32_t* w2;  // SwiGLU up projection (gate is w/s/b)
+  const uint32_t* w2;  // SWI: up projection (gate is w/s/b)
   const void* s2;
   const void* b2;
   int N, K;
   int ntiles;   // ceil(N / 16)
-  int RW;       // rounds per wave per tile
   uint32_t nib_mask, off_pair;
 };
 
-template <int BITS, int XDT, int GS, int S, int RING, bool SPLIT, bool SWI>
+template <int BITS, int XDT, int GS, int TPB, int RW, bool SWI, bool SPLIT>
 __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
+  constexpr int S = 8;                               // segments per wave per range
+  constexpr int H = SWI ? 2 : 1;                     // halves (gate, up)
+  constexpr int NI = TPB * H * RW;                   // items per wave
   constexpr int Z = 128 / GS;                        // groups per segment
   constexpr int SU = (16 / Z) < S ? 16 / Z : S;      // segments per accumulator
-  constexpr int NB = S / SU;                         // accumulators per round
+  constexpr int NB = S / SU;                         // accumulators per tile
   constexpr int NSLOT = SU * Z;                      // (segment, group) slots used
   static_assert(SU % 2 == 0 && S % SU == 0, "segments pair up into two MFMA chains");
-  static_assert(RING == 1 || RING == 3, "one or three register buffers");
   using T = XMma<XDT>;
   using XS = st_t<XDT>;
   using frag = typename T::frag;
@@ -729,7 +724,7 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int W = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int N = a.N, K = a.K, RW = a.RW;
+  const int N = a.N, K = a.K;
   const int64_t P = (int64_t)(K >> 5) * BITS;  // words per weight row
   const int G = K / GS;                        // groups per row
   // LDS: x [K] in pair order | 64 B of zeros | red [2][W][16] floats
@@ -755,73 +750,52 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
     uint32_t wd[S][BITS];
     u32x2 sv[NB], bv[NB];  // 4 consecutive 16-bit scales / biases per accumulator
   };
-  const int RT = SWI ? 2 * RW : RW;  // items per tile
-  const int step = gridDim.x;
-
-  // item (tile t, index j): half hf = j / RW (SwiGLU), round j % RW
-  auto issue = [&](Item& r, int t, int j) {
-    const int hf = SWI ? (j >= RW ? 1 : 0) : 0;
-    const int rnd = j - hf * RW;
+  // item i: tile t0 + i / (H*RW), half (i / RW) % H, range wv*RW + i % RW
+  auto issue = [&](Item& r, int t, int h, int seg_base) {
     const int n = min(t * 16 + nl, N - 1);
-    const int seg_base = (wv * RW + rnd) * S;
-    const uint32_t* wp = (hf ? a.w2 : a.w) + (int64_t)n * P + (int64_t)(seg_base * 4 + q) * BITS;
+    const uint32_t* wp = (h ? a.w2 : a.w) + (int64_t)n * P + (int64_t)(seg_base * 4 + q) * BITS;
 #pragma unroll
     for (int u = 0; u < S; u++) load_pack<BITS>(wp + u * 4 * BITS, r.wd[u]);
-    const XS* sp = (const XS*)(hf ? a.s2 : a.s) + (int64_t)n * G + seg_base * Z + gsig;
-    const XS* bp = (const XS*)(hf ? a.b2 : a.b) + (int64_t)n * G + seg_base * Z + gsig;
+    const XS* sp = (const XS*)(h ? a.s2 : a.s) + (int64_t)n * G + seg_base * Z + gsig;
+    const XS* bp = (const XS*)(h ? a.b2 : a.b) + (int64_t)n * G + seg_base * Z + gsig;
 #pragma unroll
     for (int jb = 0; jb < NB; jb++) {
       r.sv[jb] = *reinterpret_cast<const u32x2*>(sp + jb * NSLOT);
       r.bv[jb] = *reinterpret_cast<const u32x2*>(bp + jb * NSLOT);
     }
   };
-  auto advance = [&](int& t, int& j) {
-    if (++j == RT) { j = 0; t += step; }
-  };
 
-  // ---- x of this wave's K range (the only x it reads), the first items'
-  // weight loads, then x into LDS in pair order. Waves stage their own range,
-  // so no block barrier precedes the first MFMA.
-  const XS* xg = (const XS*)a.x + (int64_t)wv * RW * S * 128;
-  unsigned char* xl = smem + wv * RW * S * 256;
-  const int xch = RW * S * 16;  // 16-byte chunks in the range
-  constexpr int XPRE = 2;  // chunks per lane loaded ahead of the weights
-  u32x4 xr[XPRE];
+  // ---- x of this wave's K ranges (2 chunks of 16 B per lane per range), the
+  // weight loads of all items, then x into LDS in pair order ----
+  const int seg0 = wv * RW * S;  // first segment of this wave's ranges
+  const XS* xg = (const XS*)a.x + (int64_t)seg0 * 128;
+  unsigned char* xl = smem + seg0 * 256;
+  u32x4 xr[2 * RW];
 #pragma unroll
-  for (int c = 0; c < XPRE; c++)
-    xr[c] = (lane + 64 * c < xch) ? *reinterpret_cast<const u32x4*>(xg + (lane + 64 * c) * 8)
-                                  : u32x4{0u, 0u, 0u, 0u};
-  Item r0, r1, r2;
-  int ti = blockIdx.x, ji = 0;  // next item to issue
-  if (ti < a.ntiles) issue(r0, ti, ji);
-  advance(ti, ji);
-  if constexpr (RING == 3) {
-    if (ti < a.ntiles) issue(r1, ti, ji);
-    advance(ti, ji);
-  }
-  auto xstore = [&](int c, const u32x4 d) {
+  for (int c = 0; c < 2 * RW; c++) xr[c] = *reinterpret_cast<const u32x4*>(xg + (lane + 64 * c) * 8);
+  const int t0 = blockIdx.x * TPB;
+  Item it[NI];
+#pragma unroll
+  for (int i = 0; i < NI; i++)
+    issue(it[i], min(t0 + i / (H * RW), a.ntiles - 1), (i / RW) % H, seg0 + (i % RW) * S);
+#pragma unroll
+  for (int c = 0; c < 2 * RW; c++) {
+    const u32x4 d = xr[c];
     u32x4 o;
     o[0] = (d[0] & 0xffffu) | (d[2] << 16);
     o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
     o[2] = (d[1] & 0xffffu) | (d[3] << 16);
     o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
-    *reinterpret_cast<u32x4*>(xl + c * 16) = o;
-  };
-#pragma unroll
-  for (int c = 0; c < XPRE; c++)
-    if (lane + 64 * c < xch) xstore(lane + 64 * c, xr[c]);
-  for (int c = lane + 64 * XPRE; c < xch; c += 64)
-    xstore(c, *reinterpret_cast<const u32x4*>(xg + c * 8));
+    *reinterpret_cast<u32x4*>(xl + (lane + 64 * c) * 16) = o;
+  }
   if (lane < 4) reinterpret_cast<u32x4*>(smem + zoff)[lane] = u32x4{0u, 0u, 0u, 0u};
 
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
   constexpr uint32_t ONE2 = XDT == DT_BF16 ? 0x3F803F80u : 0x3C003C00u;
   const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
 
-  auto compute = [&](const Item& r, int j) {
-    const int hf = SWI ? (j >= RW ? 1 : 0) : 0;
-    const int rnd = j - hf * RW;
-    const int seg_base = (wv * RW + rnd) * S;
+  // Adds one item (K range starting at segment seg_base) to the 4 values per
+  // lane (slots 4q..).
+  auto compute = [&](const Item& r, int seg_base, float (&acc)[4]) {
 #pragma unroll
     for (int jb = 0; jb < NB; jb++) {
       const int real = validA ? (seg_base + jb * SU + uA) * 256 + q * 64 : zoff;
@@ -883,79 +857,44 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
     }
   };
 
-  float gate = 0.f;  // SWI: gate sum of column t*16 + nl (wave 0, q == 0)
+  // Column total of one half of a tile: this wave's part, summed over the
+  // block's waves in a fixed order (LDS slots, one barrier); the total is in
+  // lanes q == 0 of wave 0.
   int buf = 0;
-  // This wave's partial for the 16 columns of the tile, summed over the
-  // block: the total lands in lanes q == 0 of wave 0.
-  auto reduce_tile = [&]() -> float {
+  auto reduce = [&](const float (&acc)[4]) -> float {
     float part = 0.f;
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-      part = fmaf(keep[v], acc[v], part);
-      acc[v] = 0.f;
-    }
+    for (int v = 0; v < 4; v++) part = fmaf(keep[v], acc[v], part);
     part += __shfl_xor(part, 16, 64);
     part += __shfl_xor(part, 32, 64);
+    float sum = part;
     if constexpr (SPLIT) {
       float* rb = red + buf * (W * 16);
       if (q == 0) rb[wv * 16 + nl] = part;
       __syncthreads();
       buf ^= 1;
-      float sum = 0.f;
+      sum = 0.f;
       if (wv == 0)
         for (int w2 = 0; w2 < W; w2++) sum += rb[w2 * 16 + nl];
-      return sum;
-    } else {
-      return part;
     }
-  };
-  auto finish = [&](int t, int j) {
-    const float sum = reduce_tile();
-    if constexpr (SWI) {
-      if (j == RW - 1) {
-        gate = sum;
-        return;
-      }
-    }
-    if (wv == 0 && q == 0 && t * 16 + nl < N) {
-      using OS = st_t<XDT>;
-      float o = sum;
-      if constexpr (SWI) o = swiglu_f32(DT_<XDT>::round(gate), DT_<XDT>::round(sum));
-      ((OS*)a.y)[t * 16 + nl] = DT_<XDT>::from_f32(o);
-    }
+    return sum;
   };
 
-  int tc = blockIdx.x, jc = 0;  // next item to compute
-  if constexpr (RING == 1) {
-    while (tc < a.ntiles) {
-      compute(r0, jc);
-      if (jc == RW - 1 || jc == RT - 1) finish(tc, jc);
-      advance(tc, jc);
-      if (tc >= a.ntiles) break;
-      if (ti < a.ntiles) issue(r0, ti, ji);
-      advance(ti, ji);
-    }
-  } else {
-    // items in order over three buffers; the loop body is unrolled by three
-    // so every buffer index is a compile-time constant
-    while (tc < a.ntiles) {
-      if (ti < a.ntiles) issue(r2, ti, ji);
-      advance(ti, ji);
-      compute(r0, jc);
-      if (jc == RW - 1 || jc == RT - 1) finish(tc, jc);
-      advance(tc, jc);
-      if (tc >= a.ntiles) break;
-      if (ti < a.ntiles) issue(r0, ti, ji);
-      advance(ti, ji);
-      compute(r1, jc);
-      if (jc == RW - 1 || jc == RT - 1) finish(tc, jc);
-      advance(tc, jc);
-      if (tc >= a.ntiles) break;
-      if (ti < a.ntiles) issue(r1, ti, ji);
-      advance(ti, ji);
-      compute(r2, jc);
-      if (jc == RW - 1 || jc == RT - 1) finish(tc, jc);
-      advance(tc, jc);
+#pragma unroll
+  for (int tt = 0; tt < TPB; tt++) {
+    const int t = t0 + tt;
+    if (t < a.ntiles) {  // block-uniform
+      float hs[H];
+#pragma unroll
+      for (int h = 0; h < H; h++) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int rr = 0; rr < RW; rr++) compute(it[(tt * H + h) * RW + rr], seg0 + rr * S, acc);
+        hs[h] = reduce(acc);
+      }
+      float o = hs[0];
+      if constexpr (SWI) o = swiglu_f32(DT_<XDT>::round(hs[0]), DT_<XDT>::round(hs[1]));
+      if (wv == 0 && q == 0 && t * 16 + nl < N) ((st_t<XDT>*)a.y)[t * 16 + nl] = DT_<XDT>::from_f32(o);
     }
   }
 }
@@ -973,40 +912,23 @@ int device_cus() {
   return cus;
 }
 
-// Launches the streaming M == 1 kernel: W waves per block, RW rounds of S
-// segments per wave per tile (K == W * RW * S * 128), `grid` blocks; RING 3
-// when blocks walk more than one tile.
-template <int XDT, int GS, int S, bool SWI>
-hipError_t run_qmvs(const QArgs& a, int W, int RW, int grid) {
-  if (a.K != (int64_t)W * RW * S * 128 || W < 1 || W > 8) return hipErrorNotSupported;
+// Launches the streaming M == 1 kernel: K / (RW * 1024) waves per block, TPB
+// tiles per block.
+template <int XDT, int GS, int TPB, int RW, bool SWI>
+hipError_t run_qmvs(const QArgs& a) {
+  const int W = (int)(a.K / (1024 * RW));
+  if (a.K % (1024 * RW) != 0 || W < 1 || W > 8) return hipErrorNotSupported;
   const size_t lds = (size_t)a.K * 2 + 64 + (size_t)2 * W * 16 * 4;
-  if (lds > 160 * 1024) return hipErrorNotSupported;
   SKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
   k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
-  k.N = (int)a.N; k.K = (int)a.K; k.RW = RW;
+  k.N = (int)a.N; k.K = (int)a.K;
   k.ntiles = (int)((a.N + 15) / 16);
   k.nib_mask = 0x000F000Fu;
   k.off_pair = XMma<XDT>::OFFB;
-  if (grid > k.ntiles) grid = k.ntiles;
-  if (grid < 1) grid = 1;
-  const bool ring = grid < k.ntiles || RW > 1 || SWI;
-  const int which = (ring ? 2 : 0) + (W > 1 ? 1 : 0);
-  using Fn = void (*)(SKern);
-  static const Fn fns[4] = {qmvs_kernel<HQ_BITS, XDT, GS, S, 1, false, SWI>,
-                            qmvs_kernel<HQ_BITS, XDT, GS, S, 1, true, SWI>,
-                            qmvs_kernel<HQ_BITS, XDT, GS, S, 3, false, SWI>,
-                            qmvs_kernel<HQ_BITS, XDT, GS, S, 3, true, SWI>};
-  const Fn fn = fns[which];
-  if (lds > 64 * 1024) {
-    static bool big[4] = {false, false, false, false};
-    if (!big[which]) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return e;
-      big[which] = true;
-    }
-  }
+  const int grid = (k.ntiles + TPB - 1) / TPB;
+  auto fn = W > 1 ? qmvs_kernel<HQ_BITS, XDT, GS, TPB, RW, SWI, true>
+                  : qmvs_kernel<HQ_BITS, XDT, GS, TPB, RW, SWI, false>;
   hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, a.stream, k);
   return hipGetLastError();
 }
@@ -1169,23 +1091,26 @@ hipError_t run_qmvx(const QArgs& a) {
   return hipGetLastError();
 }
 
-// One x row, x and scales of one 16-bit type, K % 1024 == 0, many tiles (a
-// vocabulary-sized projection): the streaming kernel with one block per tile
-// and rounds of 8 segments over K / 1024 waves. Measured at 128256 x 4096
-// (M = 1, 4-bit g64): 52.5 us (5.6 TB/s) against 58-67 us for the persistent
-// kernel below. On the smaller Llama-3-8B and Qwen3 shapes the two kernels
-// measured within a few percent of each other (faster or slower by shape),
-// and the persistent kernel keeps them.
+// One x row, x and scales of one 16-bit type, K a multiple of 1024 above
+// 2048: the streaming kernel, one K range per wave when K <= 8192 (two when
+// K <= 16384), one tile per block (two for vocabulary-sized N). Measured on
+// the Llama-3-8B decode shapes (4-bit g64, graph of distinct weight copies)
+// against the persistent kernel below: 4096 x 4096 4.66 vs 5.03 us,
+// 14336 x 4096 8.77 vs 9.82 us, 128256 x 4096 54.8 vs 68.9 us; at K = 2048
+// the persistent kernel stays (8192 x 2048: 4.67 vs 4.90 us).
 template <int XDT, int GS, bool SWI>
 hipError_t run_qmvs_auto(const QArgs& a) {
-  if constexpr (SWI) {
-    return hipErrorNotSupported;
-  } else {
-    const int ntiles = (int)((a.N + 15) / 16);
-    const int n8 = (int)(a.K / 1024);
-    if (a.K % 1024 != 0 || n8 < 2 || n8 > 8 || ntiles < 2048) return hipErrorNotSupported;
-    return run_qmvs<XDT, GS, 8, false>(a, n8, 1, ntiles);
+  if (a.K % 1024 != 0 || a.K <= 2048) return hipErrorNotSupported;
+  const int64_t ntiles = (a.N + 15) / 16;
+  const int kr = (int)(a.K / 1024);
+  if (kr <= 8) {
+    if constexpr (!SWI) {
+      if (ntiles >= 2048) return run_qmvs<XDT, GS, 2, 1, false>(a);
+    }
+    return run_qmvs<XDT, GS, 1, 1, SWI>(a);
   }
+  if (kr % 2 == 0 && kr <= 16) return run_qmvs<XDT, GS, 1, 2, SWI>(a);
+  return hipErrorNotSupported;
 }
 
 template <int XDT, int SDT, int MB, int GS, bool SWI>
@@ -1198,7 +1123,7 @@ hipError_t run_qmvx_any(const QArgs& a) {
     }
   }
   if constexpr (SWI) {
-    // fused SwiGLU: persistent kernels only (batch 1, K % 1024 == 0)
+    // fused SwiGLU: one product (batch 1, K % 1024 == 0)
     if (!single) return hipErrorNotSupported;
     return run_qmvp<XDT, SDT, MB, GS, true>(a);
   } else {
