@@ -10,10 +10,10 @@ the timed region starts.
 
 Printed JSON line (one, on stdout):
   value         whole-step throughput: algorithmic bytes / step time (GB/s)
-  roofline      the qmv kernel (every launch of the step is one): algorithmic
-                bytes per launch / mean launch duration, the duration taken
-                from HIP events recorded on the replay stream around the timed
-                replays; peak = MI355X HBM3E 8 TB/s. `traffic` is the measured
+  roofline      the decode GEMV kernel (qmvs_kernel: every launch of the step
+                is one): algorithmic bytes per launch / mean launch duration,
+                the duration taken from HIP events recorded on the replay
+                stream around the timed replays; peak = MI355X HBM3E 8 TB/s. `traffic` is the measured
                 HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
                 WRITE_SIZE summary (profiles/), or null if absent.
   qmv_shapes    per-projection mean launch time and GB/s (graph of the 32
@@ -510,7 +510,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": round(traffic) if traffic else None,
-                     "kernel": "qmvp_kernel (matrix-core decode GEMV), every launch of the step",
+                     "kernel": "qmvs_kernel (streaming matrix-core decode GEMV), every launch "
+                               "of the step",
                      "bytes_per_launch": round(step.bytes / n_launch),
                      "mean_launch_us": round(mean_us, 3)},
         "cpu_baseline": cpu,
