@@ -28,6 +28,8 @@
 // halves read; X sums are computed during staging. Waves of a block split K
 // into contiguous segment ranges; partial sums are reduced through LDS in a
 // fixed order (deterministic).
+#include <type_traits>
+
 #include "hq_common.hpp"
 #include "hq_kernels.hpp"
 
@@ -675,8 +677,8 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
 }
 
 // ---------------------------------------------------------------------------
-// Streaming decode GEMV for one row of x (M == 1) with x and scales of one
-// 16-bit type: the decode case.
+// Streaming decode GEMV for MB <= 8 rows of x (M <= MB) with x and scales of
+// one 16-bit type: the decode case.
 //
 // A row tile is 16 output columns; a block takes TPB consecutive tiles. Each
 // of its W waves owns RW 8-segment (1024-element) K ranges of every tile, so
@@ -685,12 +687,14 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
 // otherwise. A wave loads its x ranges, issues the weight and scale loads of
 // all its items, stages its x in LDS in the MFMA pair order (waves stage only
 // what they read, so no block barrier precedes the first MFMA), then computes
-// the items in order. The group sums X of x come from
-// one MFMA per k-step against an all-ones operand, so staging does no
-// arithmetic. With W > 1 the partial sums of a tile meet in LDS after one
-// barrier (double-buffered slots, fixed order). Loads of a tile past the last
-// one read the last tile again (never computed): the issue code stays
-// straight, so waiting for one tile's loads does not wait for the next's.
+// the items in order. The A rows of one accumulator are the slots
+// (segment u, group h, x row m) of SU segments (row (u*Z + h)*MB + m), as in
+// the persistent kernel below. The group sums X of x come from one MFMA per
+// k-step against an all-ones operand, so staging does no arithmetic. With
+// W > 1 the partial sums of a tile meet in LDS after one barrier
+// (double-buffered slots, fixed order). Loads of a tile past the last one read
+// the last tile again (never computed): the issue code stays straight, so
+// waiting for one tile's loads does not wait for the next's.
 // ---------------------------------------------------------------------------
 struct SKern {
   void* y;
@@ -701,21 +705,23 @@ struct SKern {
   const uint32_t* w2;  // SWI: up projection (gate is w/s/b)
   const void* s2;
   const void* b2;
-  int N, K;
+  int M, N, K;
   int ntiles;   // ceil(N / 16)
   uint32_t nib_mask, off_pair;
 };
 
-template <int BITS, int XDT, int GS, int TPB, int RW, bool SWI, bool SPLIT>
+template <int BITS, int XDT, int GS, int MB, int TPB, int RW, bool SWI, bool SPLIT>
 __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
   constexpr int S = 8;                               // segments per wave per range
   constexpr int H = SWI ? 2 : 1;                     // halves (gate, up)
   constexpr int NI = TPB * H * RW;                   // items per wave
   constexpr int Z = 128 / GS;                        // groups per segment
-  constexpr int SU = (16 / Z) < S ? 16 / Z : S;      // segments per accumulator
-  constexpr int NB = S / SU;                         // accumulators per tile
+  constexpr int SU = (16 / (Z * MB)) < S ? 16 / (Z * MB) : S;  // segments per accumulator
+  constexpr int NB = S / SU;                         // accumulators per range
   constexpr int NSLOT = SU * Z;                      // (segment, group) slots used
-  static_assert(SU % 2 == 0 && S % SU == 0, "segments pair up into two MFMA chains");
+  constexpr int NG = MB >= 4 ? 1 : 4 / MB;           // groups per lane per accumulator
+  constexpr int MV = MB < 4 ? MB : 4;                // x rows per lane
+  static_assert(Z * MB <= 16 && S % SU == 0, "slots must fit 16 MFMA rows");
   using T = XMma<XDT>;
   using XS = st_t<XDT>;
   using frag = typename T::frag;
@@ -724,31 +730,34 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int W = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int N = a.N, K = a.K;
+  const int M = a.M, N = a.N, K = a.K;
   const int64_t P = (int64_t)(K >> 5) * BITS;  // words per weight row
   const int G = K / GS;                        // groups per row
-  // LDS: x [K] in pair order | 64 B of zeros | red [2][W][16] floats
-  const int zoff = K * 2;
+  // LDS: x [M][K] in pair order | 64 B of zeros | red [2][W][MB][16] floats
+  const int zoff = M * K * 2;
   float* red = reinterpret_cast<float*>(smem + zoff + 64);
 
   const int nl = lane & 15, q = lane >> 4;
-  // A side: A row nl is slot nl = (segment uA of the accumulator, group hA);
-  // the lane feeds k-block q of that segment when the block lies in group hA.
-  const int uA = nl / Z, hA = nl % Z;
-  const bool validA = (hA == q * Z / 4) && (nl < NSLOT);
-  // D side: value v of this lane is slot 4q + v; its group is g0 + v.
-  const int gsig = (4 * q < NSLOT) ? 4 * q : 0;
+  // A side: A row nl is slot sigA = (segment uA, group hA) of x row mA; the
+  // lane feeds k-block q of that segment when the block lies in group hA.
+  const int sigA = nl / MB, mA = nl % MB;
+  const int uA = sigA / Z, hA = sigA % Z;
+  const bool validA = (hA == q * Z / 4) && (sigA < NSLOT) && (mA < M);
+  // D side: value v of this lane is row 4q + v = slot (4q + v) / MB, x row
+  // (4q + v) % MB; the lane's groups start at slot gsig.
+  const int gsig = (4 * q) / MB < NSLOT ? (4 * q) / MB : 0;
   float keep[4];
 #pragma unroll
-  for (int v = 0; v < 4; v++) keep[v] = (4 * q + v < NSLOT) ? 1.f : 0.f;
+  for (int v = 0; v < 4; v++) keep[v] = ((4 * q + v) / MB < NSLOT) ? 1.f : 0.f;
 
   const uint32_t mask_s = a.nib_mask;
   uint32_t off_v;
   asm("v_mov_b32 %0, %1" : "=v"(off_v) : "s"(a.off_pair));
 
+  using SV = typename std::conditional<NG == 4, u32x2, typename std::conditional<NG == 2, uint32_t, uint16_t>::type>::type;
   struct Item {
     uint32_t wd[S][BITS];
-    u32x2 sv[NB], bv[NB];  // 4 consecutive 16-bit scales / biases per accumulator
+    SV sv[NB], bv[NB];  // NG consecutive 16-bit scales / biases per accumulator
   };
   // item i: tile t0 + i / (H*RW), half (i / RW) % H, range wv*RW + i % RW
   auto issue = [&](Item& r, int t, int h, int seg_base) {
@@ -760,77 +769,110 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
     const XS* bp = (const XS*)(h ? a.b2 : a.b) + (int64_t)n * G + seg_base * Z + gsig;
 #pragma unroll
     for (int jb = 0; jb < NB; jb++) {
-      r.sv[jb] = *reinterpret_cast<const u32x2*>(sp + jb * NSLOT);
-      r.bv[jb] = *reinterpret_cast<const u32x2*>(bp + jb * NSLOT);
+      r.sv[jb] = *reinterpret_cast<const SV*>(sp + jb * NSLOT);
+      r.bv[jb] = *reinterpret_cast<const SV*>(bp + jb * NSLOT);
     }
   };
 
-  // ---- x of this wave's K ranges (2 chunks of 16 B per lane per range), the
-  // weight loads of all items, then x into LDS in pair order ----
+  // ---- x of this wave's K ranges, the weight loads of all items, then x
+  // into LDS in pair order. With MB <= 2 (then M == MB) every x chunk of the
+  // wave (2 per lane per range and row) is loaded before the weights, at
+  // addresses that need no clamp, so the wait before storing them covers only
+  // these loads; more rows are loaded after the weights. ----
   const int seg0 = wv * RW * S;  // first segment of this wave's ranges
-  const XS* xg = (const XS*)a.x + (int64_t)seg0 * 128;
-  unsigned char* xl = smem + seg0 * 256;
-  u32x4 xr[2 * RW];
+  constexpr int xch = RW * S * 16;  // 16-byte chunks per x row in the ranges
+  constexpr int XPRE = MB <= 2 ? 2 * RW * MB : 0;
+  auto xsrc = [&](int c) {  // chunk c = m * xch + j of the ranges
+    const int m = c / xch, j = c - m * xch;
+    return reinterpret_cast<const u32x4*>((const XS*)a.x + (int64_t)m * K + (int64_t)seg0 * 128 + j * 8);
+  };
+  auto xstore = [&](int c, const u32x4 d) {
+    const int m = c / xch, j = c - m * xch;
+    u32x4 o;
+    o[0] = (d[0] & 0xffffu) | (d[2] << 16);
+    o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
+    o[2] = (d[1] & 0xffffu) | (d[3] << 16);
+    o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
+    *reinterpret_cast<u32x4*>(smem + (size_t)m * K * 2 + seg0 * 256 + j * 16) = o;
+  };
+  u32x4 xr[XPRE > 0 ? XPRE : 1];
 #pragma unroll
-  for (int c = 0; c < 2 * RW; c++) xr[c] = *reinterpret_cast<const u32x4*>(xg + (lane + 64 * c) * 8);
+  for (int c = 0; c < XPRE; c++) xr[c] = *xsrc(lane + 64 * c);
   const int t0 = blockIdx.x * TPB;
   Item it[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++)
     issue(it[i], min(t0 + i / (H * RW), a.ntiles - 1), (i / RW) % H, seg0 + (i % RW) * S);
 #pragma unroll
-  for (int c = 0; c < 2 * RW; c++) {
-    const u32x4 d = xr[c];
-    u32x4 o;
-    o[0] = (d[0] & 0xffffu) | (d[2] << 16);
-    o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
-    o[2] = (d[1] & 0xffffu) | (d[3] << 16);
-    o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
-    *reinterpret_cast<u32x4*>(xl + (lane + 64 * c) * 16) = o;
-  }
+  for (int c = 0; c < XPRE; c++) xstore(lane + 64 * c, xr[c]);
+  for (int c = lane + 64 * XPRE; c < M * xch; c += 64) xstore(c, *xsrc(c));
   if (lane < 4) reinterpret_cast<u32x4*>(smem + zoff)[lane] = u32x4{0u, 0u, 0u, 0u};
 
   constexpr uint32_t ONE2 = XDT == DT_BF16 ? 0x3F803F80u : 0x3C003C00u;
   const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
+  const int xrowA = (validA ? mA : 0) * K * 2;
 
   // Adds one item (K range starting at segment seg_base) to the 4 values per
-  // lane (slots 4q..).
+  // lane.
   auto compute = [&](const Item& r, int seg_base, float (&acc)[4]) {
 #pragma unroll
     for (int jb = 0; jb < NB; jb++) {
-      const int real = validA ? (seg_base + jb * SU + uA) * 256 + q * 64 : zoff;
-      // two accumulator chains (even / odd segments) so consecutive MFMAs do
-      // not wait for each other; segments are unpacked two at a time into
-      // separate registers
+      const int real = validA ? xrowA + (seg_base + jb * SU + uA) * 256 + q * 64 : zoff;
       floatx4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
       floatx4 X = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (SU >= 2) {
+        // two accumulator chains (even / odd segments) so consecutive MFMAs
+        // do not wait for each other; segments are unpacked two at a time
 #pragma unroll
-      for (int uu = 0; uu < SU; uu += 2) {
-        u32x4 av[2][4], bw[2][4];
+        for (int uu = 0; uu < SU; uu += 2) {
+          u32x4 av[2][4], bw[2][4];
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-          const int addr = (uA == uu + e) ? real : zoff;
+          for (int e = 0; e < 2; e++) {
+            const int addr = (uA == uu + e) ? real : zoff;
 #pragma unroll
-          for (int i = 0; i < 4; i++) av[e][i] = *reinterpret_cast<const u32x4*>(smem + addr + i * 16);
-        }
-#pragma unroll
-        for (int e = 0; e < 2; e++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            if constexpr (BITS == 4) {
-              const uint32_t w = r.wd[jb * SU + uu + e][i];
-              bw[e][i][0] = (w & mask_s) | off_v;
-              bw[e][i][1] = ((w >> 4) & mask_s) | off_v;
-              bw[e][i][2] = ((w >> 8) & mask_s) | off_v;
-              bw[e][i][3] = ((w >> 12) & mask_s) | off_v;
-            } else {
-              bw[e][i] = unpack_step<BITS, XDT>(r.wd[jb * SU + uu + e], i);
-            }
+            for (int i = 0; i < 4; i++) av[e][i] = *reinterpret_cast<const u32x4*>(smem + addr + i * 16);
           }
 #pragma unroll
+          for (int e = 0; e < 2; e++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              if constexpr (BITS == 4) {
+                const uint32_t w = r.wd[jb * SU + uu + e][i];
+                bw[e][i][0] = (w & mask_s) | off_v;
+                bw[e][i][1] = ((w >> 4) & mask_s) | off_v;
+                bw[e][i][2] = ((w >> 8) & mask_s) | off_v;
+                bw[e][i][3] = ((w >> 12) & mask_s) | off_v;
+              } else {
+                bw[e][i] = unpack_step<BITS, XDT>(r.wd[jb * SU + uu + e], i);
+              }
+            }
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            d0 = T::mma(__builtin_bit_cast(frag, av[0][i]), __builtin_bit_cast(frag, bw[0][i]), d0);
+            d1 = T::mma(__builtin_bit_cast(frag, av[1][i]), __builtin_bit_cast(frag, bw[1][i]), d1);
+          }
+        }
+      } else {
+        // one segment per accumulator: the two chains are its k-step halves
+        u32x4 av[4], bw[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) av[i] = *reinterpret_cast<const u32x4*>(smem + real + i * 16);
+#pragma unroll
         for (int i = 0; i < 4; i++) {
-          d0 = T::mma(__builtin_bit_cast(frag, av[0][i]), __builtin_bit_cast(frag, bw[0][i]), d0);
-          d1 = T::mma(__builtin_bit_cast(frag, av[1][i]), __builtin_bit_cast(frag, bw[1][i]), d1);
+          if constexpr (BITS == 4) {
+            const uint32_t w = r.wd[jb][i];
+            bw[i][0] = (w & mask_s) | off_v;
+            bw[i][1] = ((w >> 4) & mask_s) | off_v;
+            bw[i][2] = ((w >> 8) & mask_s) | off_v;
+            bw[i][3] = ((w >> 12) & mask_s) | off_v;
+          } else {
+            bw[i] = unpack_step<BITS, XDT>(r.wd[jb], i);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i += 2) {
+          d0 = T::mma(__builtin_bit_cast(frag, av[i]), __builtin_bit_cast(frag, bw[i]), d0);
+          d1 = T::mma(__builtin_bit_cast(frag, av[i + 1]), __builtin_bit_cast(frag, bw[i + 1]), d1);
         }
       }
       // group sums: the lane's own x (or zeros) times ones
@@ -839,43 +881,64 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
         const u32x4 xa = *reinterpret_cast<const u32x4*>(smem + real + i * 16);
         X = T::mma(__builtin_bit_cast(frag, xa), __builtin_bit_cast(frag, ones), X);
       }
-      const u32x2 sp = r.sv[jb], bp = r.bv[jb];
-      float sv[4], bv[4];
-      sv[0] = DT_<XDT>::to_f32((uint16_t)(sp[0] & 0xffffu));
-      sv[1] = DT_<XDT>::to_f32((uint16_t)(sp[0] >> 16));
-      sv[2] = DT_<XDT>::to_f32((uint16_t)(sp[1] & 0xffffu));
-      sv[3] = DT_<XDT>::to_f32((uint16_t)(sp[1] >> 16));
-      bv[0] = DT_<XDT>::to_f32((uint16_t)(bp[0] & 0xffffu));
-      bv[1] = DT_<XDT>::to_f32((uint16_t)(bp[0] >> 16));
-      bv[2] = DT_<XDT>::to_f32((uint16_t)(bp[1] & 0xffffu));
-      bv[3] = DT_<XDT>::to_f32((uint16_t)(bp[1] >> 16));
+      float sv[NG], bv[NG];
+      if constexpr (NG == 4) {
+        const u32x2 sp = r.sv[jb], bp = r.bv[jb];
+        sv[0] = DT_<XDT>::to_f32((uint16_t)(sp[0] & 0xffffu));
+        sv[1] = DT_<XDT>::to_f32((uint16_t)(sp[0] >> 16));
+        sv[2] = DT_<XDT>::to_f32((uint16_t)(sp[1] & 0xffffu));
+        sv[3] = DT_<XDT>::to_f32((uint16_t)(sp[1] >> 16));
+        bv[0] = DT_<XDT>::to_f32((uint16_t)(bp[0] & 0xffffu));
+        bv[1] = DT_<XDT>::to_f32((uint16_t)(bp[0] >> 16));
+        bv[2] = DT_<XDT>::to_f32((uint16_t)(bp[1] & 0xffffu));
+        bv[3] = DT_<XDT>::to_f32((uint16_t)(bp[1] >> 16));
+      } else if constexpr (NG == 2) {
+        sv[0] = DT_<XDT>::to_f32((uint16_t)(r.sv[jb] & 0xffffu));
+        sv[1] = DT_<XDT>::to_f32((uint16_t)(r.sv[jb] >> 16));
+        bv[0] = DT_<XDT>::to_f32((uint16_t)(r.bv[jb] & 0xffffu));
+        bv[1] = DT_<XDT>::to_f32((uint16_t)(r.bv[jb] >> 16));
+      } else {
+        sv[0] = DT_<XDT>::to_f32(r.sv[jb]);
+        bv[0] = DT_<XDT>::to_f32(r.bv[jb]);
+      }
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        const float bo = fmaf(-OFF, sv[v], bv[v]);
-        acc[v] = fmaf(sv[v], d0[v] + d1[v], fmaf(bo, X[v], acc[v]));
+        const int gi = NG == 4 ? v : (NG == 2 ? v / 2 : 0);
+        const float bo = fmaf(-OFF, sv[gi], bv[gi]);
+        acc[v] = fmaf(sv[gi], d0[v] + d1[v], fmaf(bo, X[v], acc[v]));
       }
     }
   };
 
-  // Column total of one half of a tile: this wave's part, summed over the
-  // block's waves in a fixed order (LDS slots, one barrier); the total is in
-  // lanes q == 0 of wave 0.
+  // Column totals of one half of a tile for every x row: this wave's part,
+  // summed over the block's waves in a fixed order (LDS slots, one barrier).
+  // Thread e < M*16 of the block gets row e / 16, column e % 16.
   int buf = 0;
   auto reduce = [&](const float (&acc)[4]) -> float {
-    float part = 0.f;
+    float part[MV];
 #pragma unroll
-    for (int v = 0; v < 4; v++) part = fmaf(keep[v], acc[v], part);
-    part += __shfl_xor(part, 16, 64);
-    part += __shfl_xor(part, 32, 64);
-    float sum = part;
-    if constexpr (SPLIT) {
-      float* rb = red + buf * (W * 16);
-      if (q == 0) rb[wv * 16 + nl] = part;
-      __syncthreads();
-      buf ^= 1;
-      sum = 0.f;
-      if (wv == 0)
-        for (int w2 = 0; w2 < W; w2++) sum += rb[w2 * 16 + nl];
+    for (int j = 0; j < MV; j++) part[j] = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) part[v % MV] = fmaf(keep[v], acc[v], part[v % MV]);
+#pragma unroll
+    for (int j = 0; j < MV; j++) {
+      if constexpr (MB < 8) part[j] += __shfl_xor(part[j], 16, 64);
+      part[j] += __shfl_xor(part[j], 32, 64);
+    }
+    float* rb = red + buf * (W * MB * 16);
+    if (q == 0 || (MB == 8 && q == 1)) {
+#pragma unroll
+      for (int j = 0; j < MV; j++) {
+        const int m = (MB == 8 ? 4 * q : 0) + j;
+        rb[(wv * MB + m) * 16 + nl] = part[j];
+      }
+    }
+    if constexpr (SPLIT) __syncthreads();
+    buf ^= 1;
+    float sum = 0.f;
+    if (tid < M * 16) {
+      const int m = tid >> 4, n = tid & 15;
+      for (int w2 = 0; w2 < W; w2++) sum += rb[(w2 * MB + m) * 16 + n];
     }
     return sum;
   };
@@ -894,7 +957,8 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
       }
       float o = hs[0];
       if constexpr (SWI) o = swiglu_f32(DT_<XDT>::round(hs[0]), DT_<XDT>::round(hs[1]));
-      if (wv == 0 && q == 0 && t * 16 + nl < N) ((st_t<XDT>*)a.y)[t * 16 + nl] = DT_<XDT>::from_f32(o);
+      if (tid < M * 16 && t * 16 + (tid & 15) < N)
+        ((st_t<XDT>*)a.y)[(int64_t)(tid >> 4) * N + t * 16 + (tid & 15)] = DT_<XDT>::from_f32(o);
     }
   }
 }
@@ -912,23 +976,32 @@ int device_cus() {
   return cus;
 }
 
-// Launches the streaming M == 1 kernel: K / (RW * 1024) waves per block, TPB
-// tiles per block.
-template <int XDT, int GS, int TPB, int RW, bool SWI>
+// Launches the streaming kernel: K / (RW * 1024) waves per block, TPB tiles
+// per block.
+template <int XDT, int GS, int MB, int TPB, int RW, bool SWI>
 hipError_t run_qmvs(const QArgs& a) {
   const int W = (int)(a.K / (1024 * RW));
-  if (a.K % (1024 * RW) != 0 || W < 1 || W > 8) return hipErrorNotSupported;
-  const size_t lds = (size_t)a.K * 2 + 64 + (size_t)2 * W * 16 * 4;
+  if (a.K % (1024 * RW) != 0 || W < 2 || W > 8 || a.M > MB) return hipErrorNotSupported;
+  const size_t lds = (size_t)a.M * a.K * 2 + 64 + (size_t)2 * W * MB * 16 * 4;
+  if (lds > 160 * 1024) return hipErrorNotSupported;
   SKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
   k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
-  k.N = (int)a.N; k.K = (int)a.K;
+  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
   k.ntiles = (int)((a.N + 15) / 16);
   k.nib_mask = 0x000F000Fu;
   k.off_pair = XMma<XDT>::OFFB;
   const int grid = (k.ntiles + TPB - 1) / TPB;
-  auto fn = W > 1 ? qmvs_kernel<HQ_BITS, XDT, GS, TPB, RW, SWI, true>
-                  : qmvs_kernel<HQ_BITS, XDT, GS, TPB, RW, SWI, false>;
+  auto fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true>;
+  if (lds > 64 * 1024) {
+    static bool big = false;
+    if (!big) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      if (e != hipSuccess) return e;
+      big = true;
+    }
+  }
   hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, a.stream, k);
   return hipGetLastError();
 }
@@ -1091,34 +1164,42 @@ hipError_t run_qmvx(const QArgs& a) {
   return hipGetLastError();
 }
 
-// One x row, x and scales of one 16-bit type, K a multiple of 1024 above
-// 2048: the streaming kernel, one K range per wave when K <= 8192 (two when
-// K <= 16384), one tile per block (two for vocabulary-sized N). Measured on
-// the Llama-3-8B decode shapes (4-bit g64, graph of distinct weight copies)
-// against the persistent kernel below: 4096 x 4096 4.66 vs 5.03 us,
-// 14336 x 4096 8.77 vs 9.82 us, 128256 x 4096 54.8 vs 68.9 us; at K = 2048
-// the persistent kernel stays (8192 x 2048: 4.67 vs 4.90 us).
-template <int XDT, int GS, bool SWI>
+// One or two rows of x, x and scales of one 16-bit type, K a multiple of 1024
+// above 2048: the streaming kernel, one K range per wave when K <= 8192 (two
+// when K <= 16384), one tile per block (two for vocabulary-sized N at
+// M = 1). Measured at M = 1 on the Llama-3-8B decode shapes (4-bit g64,
+// graph of distinct weight copies) against the persistent kernel below:
+// 4096 x 4096 4.66 vs 5.03 us, 14336 x 4096 8.77 vs 9.82 us, 128256 x 4096
+// 54.8 vs 68.9 us; at K = 2048 the persistent kernel stays (8192 x 2048:
+// 4.67 vs 4.90 us). At M = 2 the whole Llama-3-8B step (225 launches) takes
+// 1.63 ms here against 1.91 ms on the persistent kernel.
+template <int XDT, int GS, int MB, bool SWI>
 hipError_t run_qmvs_auto(const QArgs& a) {
-  if (a.K % 1024 != 0 || a.K <= 2048) return hipErrorNotSupported;
-  const int64_t ntiles = (a.N + 15) / 16;
-  const int kr = (int)(a.K / 1024);
-  if (kr <= 8) {
-    if constexpr (!SWI) {
-      if (ntiles >= 2048) return run_qmvs<XDT, GS, 2, 1, false>(a);
+  // M = 3..8 measured faster on the persistent kernel (its direct-x rounds):
+  // Llama-3-8B step at B = 4 2.33 vs 2.80 ms, B = 8 3.22 vs 3.63 ms.
+  if constexpr ((128 / GS) * MB > 16 || MB > 2) {
+    return hipErrorNotSupported;
+  } else {
+    if (a.K % 1024 != 0 || a.K <= 2048) return hipErrorNotSupported;
+    const int64_t ntiles = (a.N + 15) / 16;
+    const int kr = (int)(a.K / 1024);
+    if (kr <= 8) {
+      if constexpr (!SWI && MB == 1) {
+        if (ntiles >= 2048) return run_qmvs<XDT, GS, MB, 2, 1, false>(a);
+      }
+      return run_qmvs<XDT, GS, MB, 1, 1, SWI>(a);
     }
-    return run_qmvs<XDT, GS, 1, 1, SWI>(a);
+    if (kr % 2 == 0 && kr <= 16) return run_qmvs<XDT, GS, MB, 1, 2, SWI>(a);
+    return hipErrorNotSupported;
   }
-  if (kr % 2 == 0 && kr <= 16) return run_qmvs<XDT, GS, 1, 2, SWI>(a);
-  return hipErrorNotSupported;
 }
 
 template <int XDT, int SDT, int MB, int GS, bool SWI>
 hipError_t run_qmvx_any(const QArgs& a) {
   const bool single = a.batch == 1 && !a.lhs && !a.rhs;
-  if constexpr (MB == 1 && XDT == SDT) {
+  if constexpr (XDT == SDT) {
     if (single) {
-      hipError_t e = run_qmvs_auto<XDT, GS, SWI>(a);
+      hipError_t e = run_qmvs_auto<XDT, GS, MB, SWI>(a);
       if (e != hipErrorNotSupported) return e;
     }
   }

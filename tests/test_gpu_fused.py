@@ -55,6 +55,21 @@ def test_dense_hidden_fused_matches_oracle(dev, M, bits, g):
     assert rel_err(to_host_f64(h), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("K", [3072, 4096, 12288])
+@pytest.mark.parametrize("bits,g", [(4, 64), (4, 32), (8, 128)])
+def test_dense_hidden_fused_streaming(dev, M, K, bits, g):
+    # K a multiple of 1024 above 2048 at M <= 2: the streaming kernel with the
+    # gate and up halves in one block; N = 200 leaves a partial 16-row tile.
+    N, dt = 200, O.BF16
+    x, w, s, b = _dense_case(K + M * 10 + bits, M, N, K, bits, g, dt)
+    h = ops.dense_hidden_fused(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                               to_dev(b, dt, dev), N, g, bits)
+    assert tuple(h.shape) == (M, N) and h.dtype == torch.bfloat16
+    ref = _swiglu_ref(x, dt, w[:N], s[:N], b[:N], w[N:], s[N:], b[N:], g, bits)
+    assert rel_err(to_host_f64(h), ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M", [1, 8, 300])
 def test_dense_hidden_fused_f16(dev, M):
     N, K, dt, bits, g = 136, 2048, O.F16, 4, 64
@@ -66,7 +81,7 @@ def test_dense_hidden_fused_f16(dev, M):
     assert rel_err(to_host_f64(h), ref) <= 1e-2
 
 
-@pytest.mark.parametrize("M", [1, 4, 256])
+@pytest.mark.parametrize("M", [1, 2, 4, 256])
 def test_fused_equals_separate(dev, M):
     # qwen3_next.rs:13132-13169: fused gate||up == separate projections
     N, K, dt, bits, g = 512, 4096, O.BF16, 4, 64
