@@ -215,6 +215,10 @@ __global__ __launch_bounds__(256) void qmm_t_kernel(QKernM a) {
 // quarter of the tile as 8 x 8 fragments of v_mfma_f32_16x16x32 (fp32
 // accumulators). The MFMA computes the transposed product D[n][m] (A = W rows,
 // B = x rows) so every lane ends with 4 consecutive n of one m: 8-byte stores.
+// With KS > 1 a block holds KS such wave groups, each with its own LDS buffers
+// and one contiguous K / KS slice of the tile's K steps (split-K inside the
+// block, for products with too few tiles to give every CU enough waves); the
+// groups' accumulators meet in LDS and group 0 adds them in group order.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -298,18 +302,20 @@ __device__ __forceinline__ u32x4 deq8(const uint32_t (&wd)[BITS], int qq, float 
 // same columns of the up projection, arranged so that a wave's fragments
 // i < NI/2 are gate rows and i + NI/2 the matching up rows; the epilogue
 // writes swiglu(gate, up) for TN/2 columns from registers.
-template <int BITS, int CT, int GS, bool SWI, int SZ>
-__global__ __launch_bounds__(GTile<SZ>::WAVES * 64) void qgemm_kernel(GKern a) {
+template <int BITS, int CT, int GS, bool SWI, int SZ, int KS>
+__global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern a) {
   using T = Mma<CT>;
   using ST = st_t<CT>;
   using TL = GTile<SZ>;
-  constexpr int GBN = TL::TN, GBM = TL::TM, NT = TL::WAVES * 64;
+  constexpr int GBN = TL::TN, GBM = TL::TM, NT = TL::WAVES * 64;  // NT: threads per K group
   constexpr int NI = TL::WN / 16, NJ = TL::WM / 16;  // fragments per wave in n, m
   extern __shared__ __attribute__((aligned(16))) unsigned char gsm[];
-  uint16_t* As = reinterpret_cast<uint16_t*>(gsm);                    // [2][GBN][GLD]  (W)
-  uint16_t* Bs = As + 2 * GBN * GLD;                                  // [2][GBM][GLD]  (x)
+  // K group kg: threads kg*NT.., LDS buffers [2][GBN][GLD] (W) then [2][GBM][GLD] (x)
+  const int kg = KS > 1 ? (int)threadIdx.x / NT : 0;
+  uint16_t* As = reinterpret_cast<uint16_t*>(gsm) + kg * (2 * (GBN + GBM) * GLD);
+  uint16_t* Bs = As + 2 * GBN * GLD;
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = (int)threadIdx.x - kg * NT, lane = tid & 63, wv = tid >> 6;
   // wave owns n rows wn*WN.., m rows wm*WM..
   const int wn = wv / (GBM / TL::WM), wm = wv % (GBM / TL::WM);
   const int M = a.M, N = a.N, K = a.K;
@@ -404,7 +410,8 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64) void qgemm_kernel(GKern a) {
   // issued at step kt and reach LDS at step kt + kRD - 1, so kRD - 1 steps of
   // MFMAs cover their latency. (Rotating registers by copies instead would
   // make every copy wait for the loads just issued.)
-  const int nk = K / GBK;
+  const int nk = K / (GBK * KS);   // K steps of this group (the launcher checks KS | K / GBK)
+  const int kb = kg * nk * GBK;    // first K element of this group's slice
   WPre wr_[kRD];
   u32x4 xr_[kRD][4];
   auto xload_to = [&](u32x4 (&d)[4], int k0) {
@@ -419,8 +426,8 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64) void qgemm_kernel(GKern a) {
   };
 #pragma unroll
   for (int d = 0; d < kRD; d++) {
-    xload_to(xr_[d], min(d, nk - 1) * GBK);
-    wload(wr_[d], min(d, nk - 1) * GBK);
+    xload_to(xr_[d], kb + min(d, nk - 1) * GBK);
+    wload(wr_[d], kb + min(d, nk - 1) * GBK);
   }
 #pragma unroll
   for (int c = 0; c < 4; c++) wchunk(wr_[0], 0, c);
@@ -435,11 +442,36 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64) void qgemm_kernel(GKern a) {
         step(buf, wr_[(d + 1) % kRD]);
         xstore_from(xr_[(d + 1) % kRD], buf ^ 1);
         // past the end: reload the last step (unused)
-        xload_to(xr_[d], min(kt + kRD, nk - 1) * GBK);
-        wload(wr_[d], min(kt + kRD, nk - 1) * GBK);
+        xload_to(xr_[d], kb + min(kt + kRD, nk - 1) * GBK);
+        wload(wr_[d], kb + min(kt + kRD, nk - 1) * GBK);
         __syncthreads();
       }
     }
+  }
+  if constexpr (KS > 1) {
+    // groups 1.. leave their accumulators in LDS (every group has passed the
+    // last barrier of the K loop, so the staging buffers are free); group 0
+    // adds them in group order and runs the epilogue
+    floatx4* red = reinterpret_cast<floatx4*>(gsm);
+    if (kg > 0) {
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+          red[((((kg - 1) * TL::WAVES + wv) * NI + i) * NJ + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g = 1; g < KS; g++)
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+          const floatx4 o = red[((((g - 1) * TL::WAVES + wv) * NI + i) * NJ + j) * 64 + lane];
+#pragma unroll
+          for (int v = 0; v < 4; v++) acc[i][j][v] += o[v];
+        }
   }
 
   // epilogue: acc[i][j][v] = y[m][n], n = n0 + wn*WN + i*16 + 4*(lane>>4) + v,
@@ -506,15 +538,19 @@ int gemm_device_cus() {
   return cus;
 }
 
-template <int CT, int GS, bool SWI, int SZ>
+template <int CT, int GS, bool SWI, int SZ, int KS>
 hipError_t run_qgemm_sz(const QArgs& a) {
   using TL = GTile<SZ>;
+  static_assert((size_t)KS * 2 * (TL::TN + TL::TM) * GLD * 2 <= 160 * 1024, "LDS per block");
+  static_assert((size_t)(KS - 1) * TL::TN * TL::TM * 4 <= (size_t)KS * 2 * (TL::TN + TL::TM) * GLD * 2,
+                "split-K partial sums fit the staging buffers");
+  if ((a.K / GBK) % KS != 0) return hipErrorNotSupported;
   GKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
   k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
-  auto fn = qgemm_kernel<HQ_BITS, CT, GS, SWI, SZ>;
-  const size_t lds = (size_t)2 * (TL::TN + TL::TM) * GLD * 2;
+  auto fn = qgemm_kernel<HQ_BITS, CT, GS, SWI, SZ, KS>;
+  const size_t lds = (size_t)KS * 2 * (TL::TN + TL::TM) * GLD * 2;
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -524,12 +560,18 @@ hipError_t run_qgemm_sz(const QArgs& a) {
   }
   const int ont = SWI ? TL::TN / 2 : TL::TN;
   const unsigned ntiles = (unsigned)(((a.N + ont - 1) / ont) * ((a.M + TL::TM - 1) / TL::TM));
-  hipLaunchKernelGGL(fn, dim3(ntiles), dim3(TL::WAVES * 64), lds, a.stream, k);
+  hipLaunchKernelGGL(fn, dim3(ntiles), dim3(TL::WAVES * 64 * KS), lds, a.stream, k);
   return hipGetLastError();
 }
 
 // The largest tile that still gives every CU a tile: 256, else 128, else
-// 64 (each step down has 4x the tiles and less reuse per LDS byte).
+// 64 (each step down has 4x the tiles and less reuse per LDS byte). Products
+// with fewer tiles split K inside the block. Measured on random 4-bit g64
+// data (us, current choice first): M = 512 x N 2048 x K 6144 64/4 43.8 vs
+// 64/1 78.0; 512 x 6144 x 2048 128/2 35.3 vs 64/1 40.6; 256 x 14336 x 4096
+// 128/2 65.5 vs 64/1 85.3; 256 x 4096 x 14336 64/4 92.4 vs 64/1 173.7; at
+// M = 2048 the split forms were slower (4096 x 14336: 128/1 392.6 vs 128/2
+// 442.9).
 template <int CT, int GS, bool SWI>
 hipError_t run_qgemm(const QArgs& a) {
   const int cus = gemm_device_cus();
@@ -537,9 +579,15 @@ hipError_t run_qgemm(const QArgs& a) {
     const int64_t ont = SWI ? t / 2 : t;
     return ((a.N + ont - 1) / ont) * ((a.M + t - 1) / t);
   };
-  if (tiles(256) >= cus) return run_qgemm_sz<CT, GS, SWI, 256>(a);
-  if (tiles(128) >= cus) return run_qgemm_sz<CT, GS, SWI, 128>(a);
-  return run_qgemm_sz<CT, GS, SWI, 64>(a);
+  const int64_t steps = a.K / GBK;
+  if (tiles(256) >= cus) return run_qgemm_sz<CT, GS, SWI, 256, 1>(a);
+  if (tiles(128) >= cus) return run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
+  if (2 * tiles(128) >= cus)
+    return steps % 2 == 0 ? run_qgemm_sz<CT, GS, SWI, 128, 2>(a) : run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
+  const int64_t t64 = tiles(64);
+  if (t64 <= cus && steps % 4 == 0) return run_qgemm_sz<CT, GS, SWI, 64, 4>(a);
+  if (t64 <= 2 * cus && steps % 2 == 0) return run_qgemm_sz<CT, GS, SWI, 64, 2>(a);
+  return run_qgemm_sz<CT, GS, SWI, 64, 1>(a);
 }
 
 template <int CT, bool SWI = false>

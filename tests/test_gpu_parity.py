@@ -331,3 +331,14 @@ def test_two_rows_streaming(dev, dt, bits, g, N, K):
     """M = 2 with K a multiple of 1024 above 2048 (one K range per wave up to
     8192, two above); N not a multiple of the 16-row tile."""
     _qmm_check(dev, 2, N, K, bits, g, dt, dt, seed=N + K + bits * 7 + g)
+
+
+# --- prefill GEMM with K split inside the block (few output tiles) -----------
+
+@pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 4000, 1536), (512, 8000, 1024),
+                                   (256, 2048, 6144), (128, 128, 128)])
+@pytest.mark.parametrize("bits,g", [(4, 64), (3, 32), (8, 128)])
+def test_qgemm_split_k(dev, M, N, K, bits, g):
+    """Products with fewer 128-row tiles than CUs split K over 2 or 4 wave
+    groups of a block (ragged M and N included); sampled rows vs the oracle."""
+    _sampled_rows_check(dev, M, N, K, bits, g, seed=M + N + K + bits, n_rows=96)
