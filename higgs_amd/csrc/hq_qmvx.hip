@@ -681,8 +681,8 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
 // one 16-bit type: the decode case.
 //
 // A row tile is 16 output columns; a block takes TPB consecutive tiles. Each
-// of its W waves owns RW 8-segment (1024-element) K ranges of every tile, so
-// K = W * RW * 1024; an item is one (tile, half, range), where the half is the
+// of its W waves owns RW S-segment (S*128-element) K ranges of every tile, so
+// K = W * RW * S * 128; an item is one (tile, half, range), where the half is the
 // gate or the up projection of the fused SwiGLU (SWI) and there is one half
 // otherwise. A wave loads its x ranges, issues the weight and scale loads of
 // all its items, stages its x in LDS in the MFMA pair order (waves stage only
@@ -696,6 +696,11 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
 // the last tile again (never computed): the issue code stays straight, so
 // waiting for one tile's loads does not wait for the next's.
 // ---------------------------------------------------------------------------
+// Whether the streaming kernel loads every x chunk before the weights, at
+// addresses without a clamp: it then needs M == MB exactly.
+template <int MB, int S>
+constexpr bool kXPre = MB <= 2 || (MB == 4 && S == 4);
+
 struct SKern {
   void* y;
   const void* x;
@@ -710,9 +715,9 @@ struct SKern {
   uint32_t nib_mask, off_pair;
 };
 
-template <int BITS, int XDT, int GS, int MB, int TPB, int RW, bool SWI, bool SPLIT>
+template <int BITS, int XDT, int GS, int MB, int TPB, int RW, bool SWI, bool SPLIT, int S>
 __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
-  constexpr int S = 8;                               // segments per wave per range
+  static_assert(S == 4 || S == 8, "a K range is 512 or 1024 elements");  // S: segments per range
   constexpr int H = SWI ? 2 : 1;                     // halves (gate, up)
   constexpr int NI = TPB * H * RW;                   // items per wave
   constexpr int Z = 128 / GS;                        // groups per segment
@@ -775,13 +780,14 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
   };
 
   // ---- x of this wave's K ranges, the weight loads of all items, then x
-  // into LDS in pair order. With MB <= 2 (then M == MB) every x chunk of the
-  // wave (2 per lane per range and row) is loaded before the weights, at
-  // addresses that need no clamp, so the wait before storing them covers only
-  // these loads; more rows are loaded after the weights. ----
+  // into LDS in pair order. With kXPre (the launcher then requires M == MB)
+  // every x chunk of the wave (S / 4 per lane per range and row) is loaded
+  // before the weights, at addresses that need no clamp, so the wait before
+  // storing them covers only these loads; otherwise the rows are loaded after
+  // the weights. ----
   const int seg0 = wv * RW * S;  // first segment of this wave's ranges
   constexpr int xch = RW * S * 16;  // 16-byte chunks per x row in the ranges
-  constexpr int XPRE = MB <= 2 ? 2 * RW * MB : 0;
+  constexpr int XPRE = kXPre<MB, S> ? (S / 4) * RW * MB : 0;
   auto xsrc = [&](int c) {  // chunk c = m * xch + j of the ranges
     const int m = c / xch, j = c - m * xch;
     return reinterpret_cast<const u32x4*>((const XS*)a.x + (int64_t)m * K + (int64_t)seg0 * 128 + j * 8);
@@ -978,10 +984,11 @@ int device_cus() {
 
 // Launches the streaming kernel: K / (RW * 1024) waves per block, TPB tiles
 // per block.
-template <int XDT, int GS, int MB, int TPB, int RW, bool SWI>
+template <int XDT, int GS, int MB, int TPB, int RW, bool SWI, int S = 8>
 hipError_t run_qmvs(const QArgs& a) {
-  const int W = (int)(a.K / (1024 * RW));
-  if (a.K % (1024 * RW) != 0 || W < 2 || W > 8 || a.M > MB) return hipErrorNotSupported;
+  const int W = (int)(a.K / (128 * S * RW));
+  if (a.K % (128 * S * RW) != 0 || W < 2 || W > 8 || a.M > MB) return hipErrorNotSupported;
+  if (kXPre<MB, S> && a.M != MB) return hipErrorNotSupported;
   const size_t lds = (size_t)a.M * a.K * 2 + 64 + (size_t)2 * W * MB * 16 * 4;
   if (lds > 160 * 1024) return hipErrorNotSupported;
   SKern k;
@@ -992,7 +999,7 @@ hipError_t run_qmvs(const QArgs& a) {
   k.nib_mask = 0x000F000Fu;
   k.off_pair = XMma<XDT>::OFFB;
   const int grid = (k.ntiles + TPB - 1) / TPB;
-  auto fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true>;
+  auto fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true, S>;
   if (lds > 64 * 1024) {
     static bool big = false;
     if (!big) {
@@ -1175,14 +1182,24 @@ hipError_t run_qmvx(const QArgs& a) {
 // 1.63 ms here against 1.91 ms on the persistent kernel.
 template <int XDT, int GS, int MB, bool SWI>
 hipError_t run_qmvs_auto(const QArgs& a) {
-  // M = 3..8 measured faster on the persistent kernel (its direct-x rounds):
-  // Llama-3-8B step at B = 4 2.33 vs 2.80 ms, B = 8 3.22 vs 3.63 ms.
-  if constexpr ((128 / GS) * MB > 16 || MB > 2) {
+  // Llama-3-8B step: B = 2 1.53 ms (1.63 with 1024-element ranges, 1.91 on
+  // the persistent kernel); B = 4 with 512-element ranges at K = 4096 (down
+  // stays on the persistent kernel) 1.93 vs 2.34 ms. With 1024-element
+  // ranges the 4- and 8-row forms were slower than the persistent kernel
+  // (2.80 vs 2.33, 3.63 vs 3.22 ms).
+  if constexpr ((128 / GS) * MB > 16 || MB > 4) {
     return hipErrorNotSupported;
   } else {
     if (a.K % 1024 != 0 || a.K <= 2048) return hipErrorNotSupported;
     const int64_t ntiles = (a.N + 15) / 16;
     const int kr = (int)(a.K / 1024);
+    if constexpr (MB == 4) {
+      if (kr <= 4) return run_qmvs<XDT, GS, MB, 1, 1, SWI, 4>(a);  // M == 4 only
+      return hipErrorNotSupported;
+    }
+    // 512-element K ranges (twice the waves, half the work left per wave
+    // when its last weights land) for two x rows, and for one row at N <= 4096
+    if (kr <= 4 && (MB == 2 || ntiles <= 256)) return run_qmvs<XDT, GS, MB, 1, 1, SWI, 4>(a);
     if (kr <= 8) {
       if constexpr (!SWI && MB == 1) {
         if (ntiles >= 2048) return run_qmvs<XDT, GS, MB, 2, 1, false>(a);
