@@ -699,7 +699,7 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
 // Whether the streaming kernel loads every x chunk before the weights, at
 // addresses without a clamp: it then needs M == MB exactly.
 template <int MB, int S>
-constexpr bool kXPre = MB <= 2 || (MB == 4 && S == 4);
+constexpr bool kXPre = MB <= 2 || (S == 4 && (MB == 4 || MB == 8));
 
 struct SKern {
   void* y;
@@ -1183,18 +1183,21 @@ hipError_t run_qmvx(const QArgs& a) {
 template <int XDT, int GS, int MB, bool SWI>
 hipError_t run_qmvs_auto(const QArgs& a) {
   // Llama-3-8B step: B = 2 1.53 ms (1.63 with 1024-element ranges, 1.91 on
-  // the persistent kernel); B = 4 with 512-element ranges at K = 4096 (down
-  // stays on the persistent kernel) 1.93 vs 2.34 ms. With 1024-element
-  // ranges the 4- and 8-row forms were slower than the persistent kernel
-  // (2.80 vs 2.33, 3.63 vs 3.22 ms).
-  if constexpr ((128 / GS) * MB > 16 || MB > 4) {
+  // the persistent kernel); with 512-element ranges at K = 4096 (down stays
+  // on the persistent kernel) B = 4 1.93 vs 2.34 ms and B = 8 2.69 vs
+  // 3.20 ms. With 1024-element ranges the 4- and 8-row forms were slower
+  // than the persistent kernel (2.80 vs 2.33, 3.63 vs 3.22 ms).
+  if constexpr ((128 / GS) * MB > 16) {
     return hipErrorNotSupported;
   } else {
     if (a.K % 1024 != 0 || a.K <= 2048) return hipErrorNotSupported;
     const int64_t ntiles = (a.N + 15) / 16;
     const int kr = (int)(a.K / 1024);
-    if constexpr (MB == 4) {
-      if (kr <= 4) return run_qmvs<XDT, GS, MB, 1, 1, SWI, 4>(a);  // M == 4 only
+    if constexpr (MB >= 4) {
+      // M == MB only. Measured slower here than the persistent kernel, so left
+      // to it: 8 rows at vocabulary-sized N (128256 x 4096: 118.4 vs 111.0 us)
+      // and K = 14336 (4 rows, 2 ranges of 1024 per wave: 18.9 vs 15.0 us).
+      if (kr <= 4 && !(MB == 8 && ntiles >= 2048)) return run_qmvs<XDT, GS, MB, 1, 1, SWI, 4>(a);
       return hipErrorNotSupported;
     }
     // 512-element K ranges (twice the waves, half the work left per wave

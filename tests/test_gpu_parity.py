@@ -322,15 +322,16 @@ def test_wide_single_row(dev, dt, bits, g, K):
     assert err <= TOL[odt], (N, K, bits, g, dt, err)
 
 
-# --- two to four rows of x at K >= 3072 (the streaming decode kernel) ----------
+# --- two to eight rows of x at K >= 3072 (the streaming decode kernel) ---------
 
-@pytest.mark.parametrize("M", [2, 3, 4])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8])
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("bits,g", [(4, 64), (4, 32), (4, 128), (2, 64), (3, 64), (8, 64)])
 @pytest.mark.parametrize("N,K", [(301, 3072), (130, 4096), (77, 14336), (4099, 8192)])
 def test_few_rows_streaming(dev, M, dt, bits, g, N, K):
-    """M = 2..4 with K a multiple of 1024 above 2048 (512-element K ranges at
-    K <= 4096, 1024 above, two per wave above 8192); N not a multiple of the
+    """M = 2..8 with K a multiple of 1024 above 2048 (the streaming kernel:
+    512-element K ranges at K <= 4096, 1024 above, two per wave above 8192;
+    the persistent kernel where it is not used); N not a multiple of the
     16-row tile."""
     _qmm_check(dev, M, N, K, bits, g, dt, dt, seed=N + K + bits * 7 + g + M)
 
