@@ -223,7 +223,6 @@ __global__ __launch_bounds__(256) void qmm_t_kernel(QKernM a) {
 namespace {
 
 constexpr int GBM = 256, GBN = 256, GBK = 64;
-constexpr int kRD = 3;  // register prefetch depth (K-steps) of the large-tile GEMM
 
 // Tile shapes of the large-tile GEMM: a block computes TN W rows x TM x rows
 // with WAVES waves of WN x WM each. 256 x 256 (8 waves, one block per CU) is
@@ -358,20 +357,22 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   const ST* sg = (const ST*)(w_up ? a.s2 : a.s);
   const ST* bg = (const ST*)(w_up ? a.b2 : a.b);
 
+  // Scale and bias stay raw 16-bit in the ring and are widened where they are
+  // used: widening at the load makes the compiler wait for that load at once.
   struct WPre {
     uint32_t wd[BITS];
-    float sv, bv;
+    uint16_t sv, bv;
   };
   auto wload = [&](WPre& p, int k0) {
     load_pack<BITS>(wg + woff + (uint32_t)(k0 >> 5) * BITS, p.wd);
     const uint32_t gi = goff + (uint32_t)((k0 + wp * 32) / GS);
-    p.sv = DT_<CT>::load(sg, gi);
-    p.bv = DT_<CT>::load(bg, gi);
+    p.sv = sg[gi];
+    p.bv = bg[gi];
   };
   // Quarter qq (8 elements) of this thread's pack, one 16-byte LDS store.
   auto wchunk = [&](const WPre& p, int buf, int qq) {
     uint16_t* dst = As + buf * GBN * GLD + wr * GLD + wp * 32 + qq * 8;
-    *reinterpret_cast<u32x4*>(dst) = deq8<BITS, CT>(p.wd, qq, p.sv, p.bv);
+    *reinterpret_cast<u32x4*>(dst) = deq8<BITS, CT>(p.wd, qq, DT_<CT>::to_f32(p.sv), DT_<CT>::to_f32(p.bv));
   };
 
   floatx4 acc[NI][NJ];
@@ -406,10 +407,15 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   };
 
   // Register ring of kRD K-steps for x and W, indexed by compile-time slots
-  // inside an unrolled group of 2*kRD steps: the loads of step kt + kRD are
-  // issued at step kt and reach LDS at step kt + kRD - 1, so kRD - 1 steps of
-  // MFMAs cover their latency. (Rotating registers by copies instead would
-  // make every copy wait for the loads just issued.)
+  // inside an unrolled group of steps: the loads of step kt + kRD are issued
+  // at step kt and reach LDS at step kt + kRD - 1, so kRD - 1 steps of MFMAs
+  // cover their latency. (Rotating registers by copies instead would make
+  // every copy wait for the loads just issued.) Depth 2 with whole groups
+  // free of branches measured fastest (M = 2048 gate/up 300 -> 287 us, fused
+  // SwiGLU 561 -> 524 us, M = 256 and 512 2-6 % faster); the 128 x 128 tile
+  // without split-K keeps depth 3 and per-step tests, which hold it at two
+  // waves per SIMD (depth 2 unbranched took it to one: down 337 -> 347 us).
+  constexpr int kRD = (SZ == 128 && KS == 1) ? 3 : 2;
   const int nk = K / (GBK * KS);   // K steps of this group (the launcher checks KS | K / GBK)
   const int kb = kg * nk * GBK;    // first K element of this group's slice
   WPre wr_[kRD];
@@ -433,19 +439,35 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   for (int c = 0; c < 4; c++) wchunk(wr_[0], 0, c);
   xstore_from(xr_[0], 0);
   __syncthreads();
-  for (int kt0 = 0; kt0 < nk; kt0 += 2 * kRD) {
+  // One K step at position dd of a group (ring slot dd % kRD, LDS buffer
+  // dd & 1).
+  auto kstep = [&](int kt, int dd) {
+    const int d = dd % kRD, buf = dd & 1;
+    step(buf, wr_[(d + 1) % kRD]);
+    xstore_from(xr_[(d + 1) % kRD], buf ^ 1);
+    // past the end: reload the last step (unused)
+    xload_to(xr_[d], kb + min(kt + kRD, nk - 1) * GBK);
+    wload(wr_[d], kb + min(kt + kRD, nk - 1) * GBK);
+    __syncthreads();
+  };
+  if constexpr (kRD % 2 == 0) {
+    // Whole groups of kRD steps run with no branch between their steps (a
+    // load issued under a branch makes the compiler drain every load in
+    // flight at the join); the steps of a last partial group are tested one
+    // by one.
+    int kt0 = 0;
+    for (; kt0 + kRD <= nk; kt0 += kRD) {
 #pragma unroll
-    for (int dd = 0; dd < 2 * kRD; dd++) {
-      const int kt = kt0 + dd;
-      if (kt < nk) {
-        const int d = dd % kRD, buf = dd & 1;
-        step(buf, wr_[(d + 1) % kRD]);
-        xstore_from(xr_[(d + 1) % kRD], buf ^ 1);
-        // past the end: reload the last step (unused)
-        xload_to(xr_[d], kb + min(kt + kRD, nk - 1) * GBK);
-        wload(wr_[d], kb + min(kt + kRD, nk - 1) * GBK);
-        __syncthreads();
-      }
+      for (int dd = 0; dd < kRD; dd++) kstep(kt0 + dd, dd);
+    }
+#pragma unroll
+    for (int dd = 0; dd < kRD - 1; dd++)
+      if (kt0 + dd < nk) kstep(kt0 + dd, dd);
+  } else {
+    for (int kt0 = 0; kt0 < nk; kt0 += 2 * kRD) {
+#pragma unroll
+      for (int dd = 0; dd < 2 * kRD; dd++)
+        if (kt0 + dd < nk) kstep(kt0 + dd, dd);
     }
   }
   if constexpr (KS > 1) {
