@@ -715,7 +715,7 @@ struct SKern {
   uint32_t nib_mask, off_pair;
 };
 
-template <int BITS, int XDT, int GS, int MB, int TPB, int RW, bool SWI, bool SPLIT, int S>
+template <int BITS, int XDT, int GS, int MB, int TPB, int RW, bool SWI, bool SPLIT, int S, bool XF>
 __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
   static_assert(S == 4 || S == 8, "a K range is 512 or 1024 elements");  // S: segments per range
   constexpr int H = SWI ? 2 : 1;                     // halves (gate, up)
@@ -826,6 +826,19 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
       const int real = validA ? xrowA + (seg_base + jb * SU + uA) * 256 + q * 64 : zoff;
       floatx4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
       floatx4 X = {0.f, 0.f, 0.f, 0.f};
+      // group sums: the lane's own x (or zeros) times ones. With XF they go
+      // first, while the item's weights are still arriving (4096 x 4096,
+      // 512-element ranges: 4.50 -> 4.22 us); for large N that order measured
+      // slower (14336 x 4096: 8.86 -> 10.07 us at M = 1, 9.5 -> 10.5 us at
+      // M = 2), so there they go last.
+      auto group_sums = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const u32x4 xa = *reinterpret_cast<const u32x4*>(smem + real + i * 16);
+          X = T::mma(__builtin_bit_cast(frag, xa), __builtin_bit_cast(frag, ones), X);
+        }
+      };
+      if constexpr (XF) group_sums();
       if constexpr (SU >= 2) {
         // two accumulator chains (even / odd segments) so consecutive MFMAs
         // do not wait for each other; segments are unpacked two at a time
@@ -881,12 +894,7 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
           d1 = T::mma(__builtin_bit_cast(frag, av[i + 1]), __builtin_bit_cast(frag, bw[i + 1]), d1);
         }
       }
-      // group sums: the lane's own x (or zeros) times ones
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const u32x4 xa = *reinterpret_cast<const u32x4*>(smem + real + i * 16);
-        X = T::mma(__builtin_bit_cast(frag, xa), __builtin_bit_cast(frag, ones), X);
-      }
+      if constexpr (!XF) group_sums();
       float sv[NG], bv[NG];
       if constexpr (NG == 4) {
         const u32x2 sp = r.sv[jb], bp = r.bv[jb];
@@ -984,7 +992,7 @@ int device_cus() {
 
 // Launches the streaming kernel: K / (RW * 1024) waves per block, TPB tiles
 // per block.
-template <int XDT, int GS, int MB, int TPB, int RW, bool SWI, int S = 8>
+template <int XDT, int GS, int MB, int TPB, int RW, bool SWI, int S = 8, bool XF = false>
 hipError_t run_qmvs(const QArgs& a) {
   const int W = (int)(a.K / (128 * S * RW));
   if (a.K % (128 * S * RW) != 0 || W < 2 || W > 8 || a.M > MB) return hipErrorNotSupported;
@@ -999,7 +1007,7 @@ hipError_t run_qmvs(const QArgs& a) {
   k.nib_mask = 0x000F000Fu;
   k.off_pair = XMma<XDT>::OFFB;
   const int grid = (k.ntiles + TPB - 1) / TPB;
-  auto fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true, S>;
+  auto fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true, S, XF>;
   if (lds > 64 * 1024) {
     static bool big = false;
     if (!big) {
@@ -1193,24 +1201,31 @@ hipError_t run_qmvs_auto(const QArgs& a) {
     if (a.K % 1024 != 0 || a.K <= 2048) return hipErrorNotSupported;
     const int64_t ntiles = (a.N + 15) / 16;
     const int kr = (int)(a.K / 1024);
+    // 512-element K ranges (twice the waves, half the work left per wave
+    // when its last weights land) at K <= 4096 for several x rows, and for one
+    // row at N <= 4096; group sums first at N <= 4096. Several rows need
+    // M == MB (the launcher checks it).
+    const bool small_n = ntiles <= 256;
+    if (kr <= 4 && (small_n || MB >= 2)) {
+      // 8 rows at vocabulary-sized N measured slower here than on the
+      // persistent kernel (128256 x 4096: 118.4 vs 111.0 us)
+      if (MB == 8 && ntiles >= 2048) return hipErrorNotSupported;
+      return small_n ? run_qmvs<XDT, GS, MB, 1, 1, SWI, 4, true>(a) : run_qmvs<XDT, GS, MB, 1, 1, SWI, 4>(a);
+    }
     if constexpr (MB >= 4) {
-      // M == MB only. Measured slower here than the persistent kernel, so left
-      // to it: 8 rows at vocabulary-sized N (128256 x 4096: 118.4 vs 111.0 us)
-      // and K = 14336 (4 rows, 2 ranges of 1024 per wave: 18.9 vs 15.0 us).
-      if (kr <= 4 && !(MB == 8 && ntiles >= 2048)) return run_qmvs<XDT, GS, MB, 1, 1, SWI, 4>(a);
+      // K > 4096 at 4 and 8 rows stays on the persistent kernel (4 rows,
+      // 14336: two 1024-element ranges per wave 18.9 vs 15.0 us)
+      return hipErrorNotSupported;
+    } else {
+      if (kr <= 8) {
+        if constexpr (!SWI && MB == 1) {
+          if (ntiles >= 2048) return run_qmvs<XDT, GS, MB, 2, 1, false>(a);
+        }
+        return run_qmvs<XDT, GS, MB, 1, 1, SWI>(a);
+      }
+      if (kr % 2 == 0 && kr <= 16) return run_qmvs<XDT, GS, MB, 1, 2, SWI>(a);
       return hipErrorNotSupported;
     }
-    // 512-element K ranges (twice the waves, half the work left per wave
-    // when its last weights land) for two x rows, and for one row at N <= 4096
-    if (kr <= 4 && (MB == 2 || ntiles <= 256)) return run_qmvs<XDT, GS, MB, 1, 1, SWI, 4>(a);
-    if (kr <= 8) {
-      if constexpr (!SWI && MB == 1) {
-        if (ntiles >= 2048) return run_qmvs<XDT, GS, MB, 2, 1, false>(a);
-      }
-      return run_qmvs<XDT, GS, MB, 1, 1, SWI>(a);
-    }
-    if (kr % 2 == 0 && kr <= 16) return run_qmvs<XDT, GS, MB, 1, 2, SWI>(a);
-    return hipErrorNotSupported;
   }
 }
 
