@@ -226,12 +226,15 @@ constexpr int GBM = 256, GBN = 256, GBK = 64;
 
 // Tile shapes of the large-tile GEMM: a block computes TN W rows x TM x rows
 // with WAVES waves of WN x WM each. 256 x 256 (8 waves, one block per CU) is
-// the main shape; 128 x 128 (4 waves, two blocks per CU) is for products
-// whose 256-tiles would leave CUs idle (M = 2048 down: 128 tiles for 256
-// CUs).
+// the main shape; 256 x 128 (id 384, 8 waves) and 128 x 128 (4 waves, two
+// blocks per CU) are for products whose 256-tiles would leave CUs idle
+// (M = 2048 down: 128 256-tiles for 256 CUs).
 template <int SZ> struct GTile;
 template <> struct GTile<256> {
   static constexpr int TN = 256, TM = 256, WAVES = 8, WN = 128, WM = 64;
+};
+template <> struct GTile<384> {
+  static constexpr int TN = 256, TM = 128, WAVES = 8, WN = 64, WM = 64;
 };
 template <> struct GTile<128> {
   static constexpr int TN = 128, TM = 128, WAVES = 4, WN = 64, WM = 64;
@@ -335,16 +338,17 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   const int64_t G = K / GS;
   const ST* xg = (const ST*)a.x;
 
-  // x tile (GBM x 64): thread copies rows xr + (NT/8)j (j < 4), 16-byte chunk
-  // xc. Rows past M read row M-1 (never stored), so every load is
+  // x tile (GBM x 64): thread copies rows xr + (NT/8)j (j < XJ), 16-byte
+  // chunk xc. Rows past M read row M-1 (never stored), so every load is
   // unconditional.
+  constexpr int XJ = GBM / (NT / 8);
   const int xr = tid >> 3, xc = tid & 7;
-  static_assert(GBM == 4 * (NT / 8) && GBN == NT / 2, "thread maps cover the tiles");
+  static_assert(GBM == XJ * (NT / 8) && GBN == NT / 2, "thread maps cover the tiles");
   // W tile (GBN x 64): thread dequantizes pack wp of row wr.
   const int wr = tid >> 1, wp = tid & 1;
-  uint32_t xoff[4];  // element offsets into x (the launcher checks M*K < 2^31)
+  uint32_t xoff[XJ];  // element offsets into x (the launcher checks M*K < 2^31)
 #pragma unroll
-  for (int j = 0; j < 4; j++)
+  for (int j = 0; j < XJ; j++)
     xoff[j] = (uint32_t)min(m0 + xr + (NT / 8) * j, M - 1) * (uint32_t)K + xc * 8;
   // SWI: tile row wr is column n0 + (wr / WN) * WN/2 + wr % (WN/2) of the gate
   // (wr % WN < WN/2) or of the up projection.
@@ -419,15 +423,15 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   const int nk = K / (GBK * KS);   // K steps of this group (the launcher checks KS | K / GBK)
   const int kb = kg * nk * GBK;    // first K element of this group's slice
   WPre wr_[kRD];
-  u32x4 xr_[kRD][4];
-  auto xload_to = [&](u32x4 (&d)[4], int k0) {
+  u32x4 xr_[kRD][XJ];
+  auto xload_to = [&](u32x4 (&d)[XJ], int k0) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) d[j] = *reinterpret_cast<const u32x4*>(xg + xoff[j] + k0);
+    for (int j = 0; j < XJ; j++) d[j] = *reinterpret_cast<const u32x4*>(xg + xoff[j] + k0);
   };
-  auto xstore_from = [&](const u32x4 (&d)[4], int buf) {
+  auto xstore_from = [&](const u32x4 (&d)[XJ], int buf) {
     uint16_t* bs = Bs + buf * GBM * GLD;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < XJ; j++)
       *reinterpret_cast<u32x4*>(bs + (xr + (NT / 8) * j) * GLD + xc * 8) = d[j];
   };
 #pragma unroll
@@ -597,12 +601,16 @@ hipError_t run_qgemm_sz(const QArgs& a) {
 template <int CT, int GS, bool SWI>
 hipError_t run_qgemm(const QArgs& a) {
   const int cus = gemm_device_cus();
-  auto tiles = [&](int64_t t) {
-    const int64_t ont = SWI ? t / 2 : t;
-    return ((a.N + ont - 1) / ont) * ((a.M + t - 1) / t);
+  auto tiles2 = [&](int64_t tn, int64_t tm) {
+    const int64_t ont = SWI ? tn / 2 : tn;
+    return ((a.N + ont - 1) / ont) * ((a.M + tm - 1) / tm);
   };
+  auto tiles = [&](int64_t t) { return tiles2(t, t); };
   const int64_t steps = a.K / GBK;
   if (tiles(256) >= cus) return run_qgemm_sz<CT, GS, SWI, 256, 1>(a);
+  // 256 x 128 before 128 x 128: one 8-wave block per CU instead of two
+  // 4-wave blocks, half the x tile loads (M = 2048 down 341 -> 306 us)
+  if (tiles2(256, 128) >= cus) return run_qgemm_sz<CT, GS, SWI, 384, 1>(a);
   if (tiles(128) >= cus) return run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
   if (2 * tiles(128) >= cus)
     return steps % 2 == 0 ? run_qgemm_sz<CT, GS, SWI, 128, 2>(a) : run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
