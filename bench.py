@@ -27,6 +27,9 @@ Printed JSON line (one, on stdout):
   configs       configs[0] (Llama-3.2-1B up-proj qmv at B=1) and configs[3]
                 (Qwen3-1.7B gate/up and down at bits 2/3/8 g64 and 4-bit
                 g32/g128, B=1 GB/s and M=512 TFLOP/s)
+  dequant       dequantize of whole 4-bit g64 tensors (configs[0] shape and
+                the Llama-3-8B gate), GB/s of bytes read + written, and the
+                quantized embedding (take + dequantize) of 512 token rows
   decode_fused  the same decode step with the launches fused: q|k|v
                 concatenated (one launch), gate/up + SwiGLU in one launch
                 (hq_quantized_matmul_swiglu, the reference's
@@ -352,6 +355,60 @@ def bench_configs(dev, steps):
     return out
 
 
+def bench_dequant(dev, steps):
+    """dequantize (a6): whole tensors at the configs[0] and Llama-3-8B gate
+    shapes over distinct copies (more than the 256 MB Infinity Cache), bytes =
+    packed W + scales/biases read + bf16 out written; and the quantized
+    embedding (take then dequantize) of 512 token rows of a Llama-3-8B
+    vocabulary table."""
+    import numpy as np
+    import torch
+
+    from higgs_amd import _lib, gen
+
+    lib = _lib.lib()
+    out = {}
+
+    def whole(tag, N, K, copies):
+        ws = [gen.torch_quantized(700 + c, N, K, BITS, GROUP, dev) for c in range(copies)]
+        y = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+
+        def run(stream, ws=ws):
+            for (w, s, b) in ws:
+                _lib.check(lib.hq_dequantize(y.data_ptr(), w.data_ptr(), s.data_ptr(),
+                                             b.data_ptr(), N, K, GROUP, BITS, 2, stream))
+        ms = time_graph(run, steps, 1, dev) / len(ws)
+        nbytes = N * K * BITS // 8 + 2 * N * (K // GROUP) * 2 + N * K * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[tag] = {"rows": N, "K": K, "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del ws
+
+    whole("c0_8192x2048", 8192, 2048, 32)
+    whole("gate_14336x4096", 14336, 4096, 8)
+    # embedding: 32 batches of 512 token ids into a [128256, 4096] table (one
+    # graph of 32 launches: a single small launch per replay would time the
+    # host's graph launch instead)
+    w, s, b = gen.torch_quantized(777, VOCAB, HIDDEN, BITS, GROUP, dev)
+    nb = 32
+    ids = torch.from_numpy(np.random.default_rng(5).integers(0, VOCAB, (nb, 512))
+                           .astype(np.uint32).view(np.int32)).to(dev)
+    e = torch.empty((512, HIDDEN), dtype=torch.bfloat16, device=dev)
+
+    def run_e(stream):
+        for i in range(nb):
+            _lib.check(lib.hq_embedding_dequantize(e.data_ptr(), w.data_ptr(), s.data_ptr(),
+                                                   b.data_ptr(), ids[i].data_ptr(), 512, VOCAB,
+                                                   HIDDEN, GROUP, BITS, 2, stream))
+    ms = time_graph(run_e, steps, 1, dev) / nb
+    nbytes = 512 * (HIDDEN * BITS // 8 + 2 * (HIDDEN // GROUP) * 2 + 4 + HIDDEN * 2)
+    out["embedding_512_of_128256x4096"] = {"tokens": 512, "us": round(ms * 1e3, 3),
+                                           "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    del w, s, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(model, B, target_s):
     """Oracle quantized_matmul (MLX-CPU-style restatement, oracle/hq_oracle.c
     hqo_qmm_mlx) on the host, over layer 0's seven projections at batch B."""
@@ -470,6 +527,8 @@ def main():
         log(f"[bench] moe: {extras['moe']}")
         extras["configs"] = bench_configs(dev, max(3, args.steps // 4))
         log(f"[bench] configs: {extras['configs']}")
+        extras["dequant"] = bench_dequant(dev, max(3, args.steps // 4))
+        log(f"[bench] dequant: {extras['dequant']}")
         fp = FusedPlan(model, args.batch, dev)
         mf = time_graph(fp.run, args.steps, 2, dev)
         extras["decode_fused"] = {"batch": args.batch, "launches": len(fp.calls),

@@ -23,6 +23,51 @@ __device__ __forceinline__ float deq_round(uint32_t q, float s, float b) {
   return DT_<SDT>::round(p + b);
 }
 
+// Two adjacent 16-bit outputs round(round(q*s) + b), packed. The roundings
+// are the hardware float -> bf16 / fp16 conversions (round to nearest even,
+// v_cvt_pk_bf16_f32 / v_cvt_f16_f32), a third of the instructions of the
+// integer rounding sequence; NaN results are rewritten to the canonical
+// quiet NaN (bf16 0x7fc0; fp16 sign | 0x7e00) exactly as the integer
+// sequence produces them. A NaN needs a non-finite scale or bias (q*s of
+// finite values at most overflows to an infinity, and inf + finite is inf),
+// so CANON = false skips the rewrite for groups whose scale and bias are
+// finite.
+template <int SDT, bool CANON>
+__device__ __forceinline__ uint32_t deq_pair(uint32_t q0, uint32_t q1, float s, float b) {
+#pragma clang fp contract(off)
+  if constexpr (SDT == DT_BF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    bf2 p;
+    p[0] = (__bf16)((float)q0 * s);
+    p[1] = (__bf16)((float)q1 * s);
+    const float r0 = (float)p[0] + b, r1 = (float)p[1] + b;
+    bf2 o;
+    o[0] = (__bf16)r0;
+    o[1] = (__bf16)r1;
+    uint32_t u = __builtin_bit_cast(uint32_t, o);
+    if constexpr (CANON) {
+      if (r0 != r0) u = (u & 0xffff0000u) | 0x7fc0u;
+      if (r1 != r1) u = (u & 0x0000ffffu) | 0x7fc00000u;
+    }
+    return u;
+  } else {
+    // The product is exact in fp32 (at most 8 + 11 significant bits). The
+    // empty asm keeps it a plain fp32 multiply: fused into v_fma_mixlo_f16
+    // (q * s + 0) it would turn a -0 product into +0.
+    float m0 = (float)q0 * s, m1 = (float)q1 * s;
+    __asm__ volatile("" : "+v"(m0), "+v"(m1));
+    const _Float16 p0 = (_Float16)m0, p1 = (_Float16)m1;
+    const float r0 = (float)p0 + b, r1 = (float)p1 + b;
+    uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)r0);
+    uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)r1);
+    if constexpr (CANON) {
+      if (r0 != r0) lo = ((__float_as_uint(r0) >> 16) & 0x8000u) | 0x7e00u;
+      if (r1 != r1) hi = ((__float_as_uint(r1) >> 16) & 0x8000u) | 0x7e00u;
+    }
+    return lo | (hi << 16);
+  }
+}
+
 template <int BITS, int SDT>
 __global__ __launch_bounds__(256) void dequant_kernel(st_t<SDT>* __restrict__ out,
                                                        const uint32_t* __restrict__ w,
@@ -66,11 +111,14 @@ __global__ __launch_bounds__(256) void dequant_kernel(st_t<SDT>* __restrict__ ou
         load_pack<BITS>(w + src * P + (int64_t)p * BITS, wd);
         const int64_t gi = src * G + (p >> gshift_packs);
         const float sv = DT_<SDT>::load(s, gi), bv = DT_<SDT>::load(b, gi);
+        if (__builtin_isfinite(sv) && __builtin_isfinite(bv)) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-          uint32_t lo = DT_<SDT>::from_f32(deq_round<SDT>(pack_elem<BITS>(wd, 2 * i), sv, bv));
-          uint32_t hi = DT_<SDT>::from_f32(deq_round<SDT>(pack_elem<BITS>(wd, 2 * i + 1), sv, bv));
-          h[i] = lo | (hi << 16);
+          for (int i = 0; i < 16; i++)
+            h[i] = deq_pair<SDT, false>(pack_elem<BITS>(wd, 2 * i), pack_elem<BITS>(wd, 2 * i + 1), sv, bv);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; i++)
+            h[i] = deq_pair<SDT, true>(pack_elem<BITS>(wd, 2 * i), pack_elem<BITS>(wd, 2 * i + 1), sv, bv);
         }
       }
       u32x4* o4 = reinterpret_cast<u32x4*>(o);

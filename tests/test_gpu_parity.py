@@ -50,6 +50,47 @@ def test_dequantize_bit_exact(dev, bits, g, dt):
     np.testing.assert_array_equal(to_host_bits(out), ref)
 
 
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequantize_special_values_bit_exact(dev, dt, bits):
+    """Scales and biases at NaN (both signs, odd payloads), +-Inf, the largest
+    finite value (products overflow), denormals, signed zeros. Every non-NaN
+    output bit equals the oracle's and every NaN output is a NaN where the
+    oracle's is: the sign of a NaN made by an invalid operation (Inf * 0,
+    Inf - Inf) is the platform's default NaN (negative on x86, where the
+    oracle runs; positive on the GPU), not a property of the algorithm."""
+    if dt == O.BF16:
+        special = [0x7fc0, 0xffc1, 0x7f81, 0x7f80, 0xff80, 0x7f7f, 0xff7f, 0x0001, 0x8003,
+                   0x0080, 0x0000, 0x8000, 0x3f80, 0xbf80, 0x3c00, 0x0040]
+    else:
+        special = [0x7e00, 0xfe01, 0x7c01, 0x7c00, 0xfc00, 0x7bff, 0xfbff, 0x0001, 0x8003,
+                   0x0400, 0x0000, 0x8000, 0x3c00, 0xbc00, 0x2000, 0x0200]
+    rows, K, g = 16, 256, 32
+    G = K // g
+    rng = np.random.default_rng(bits)
+    sp = np.array(special, dtype=np.uint16)
+    s = sp[rng.integers(0, len(sp), (rows, G))]
+    b = sp[rng.integers(0, len(sp), (rows, G))]
+    s[0, :] = sp[:G]            # every special value as a scale and as a bias
+    b[1, :] = sp[:G]
+    s[2, :] = sp[G:2 * G] if len(sp) >= 2 * G else sp[:G]
+    b[3, :] = sp[G:2 * G] if len(sp) >= 2 * G else sp[:G]
+    q = rng.integers(0, 1 << bits, (rows, K), dtype=np.uint64)
+    q[:, :4] = 0                # 0 * Inf
+    w = gen.pack_bits(q, bits)
+    out = to_host_bits(ops.dequantize(words_dev(w, dev), to_dev(s, dt, dev), to_dev(b, dt, dev),
+                                      g, bits))
+    ref = O.dequantize(w, s, b, g, bits, dt)
+    exp_mask, man_mask = (0x7f80, 0x007f) if dt == O.BF16 else (0x7c00, 0x03ff)
+    isnan = lambda u: ((u & exp_mask) == exp_mask) & ((u & man_mask) != 0)
+    np.testing.assert_array_equal(isnan(out), isnan(ref))
+    assert isnan(ref).any() and (~isnan(ref)).any()
+    np.testing.assert_array_equal(out[~isnan(ref)], ref[~isnan(ref)])
+    # NaN outputs are canonical quiet NaNs
+    nan_bits = out[isnan(out)] & 0x7fff
+    assert np.all(nan_bits == (0x7fc0 if dt == O.BF16 else 0x7e00))
+
+
 def test_dequantize_bit_exact_c0_shape(dev):
     # configs[0]: [8192, 2048] 4-bit g64, bf16 scales
     w, s, b = quant(1, 8192, 2048, 4, 64, O.BF16)
