@@ -209,7 +209,7 @@ static int deq_common(const char* tag, void* out, const uint32_t* w, const void*
                 "[%s] Invalid sizes rows=%lld K=%lld: K must be a positive multiple of the group "
                 "size %d.",
                 tag, (long long)(idx ? n : rows), (long long)K, group_size);
-  if ((n * (K / 32)) >= ((int64_t)1 << 31))
+  if ((n * (K / 32)) >= ((int64_t)1 << 29))  // 4 threads per 32-element pack, 32-bit indices
     return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] Too many elements (%lld x %lld).", tag,
                 (long long)n, (long long)K);
   if (n == 0) return HQ_OK;

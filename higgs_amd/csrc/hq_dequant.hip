@@ -128,6 +128,71 @@ __global__ __launch_bounds__(256) void dequant_kernel(st_t<SDT>* __restrict__ ou
   }
 }
 
+// 16-bit outputs: one thread per 8 consecutive outputs (a quarter of a
+// 32-element pack), so a wave's 16-byte stores cover 1 KB contiguously and
+// its weight loads are contiguous too (BITS bytes per thread). The thread
+// reads the 8*BITS bits of its quarter from at most two words of the pack.
+template <int BITS, int SDT>
+__global__ __launch_bounds__(256) void dequant8_kernel(uint16_t* __restrict__ out,
+                                                        const uint32_t* __restrict__ w,
+                                                        const uint16_t* __restrict__ s,
+                                                        const uint16_t* __restrict__ b,
+                                                        const uint32_t* __restrict__ rows_idx,
+                                                        uint32_t total_q, uint32_t ppr,
+                                                        int64_t src_rows, int gshift_packs) {
+  const int64_t K = (int64_t)ppr * 32;
+  const int64_t P = (int64_t)ppr * BITS;
+  const int64_t G = (int64_t)ppr >> gshift_packs;
+  for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < total_q; t += gridDim.x * 256u) {
+    const uint32_t pk = t >> 2, qq = t & 3u;
+    const uint32_t r = pk / ppr;
+    const uint32_t p = pk - r * ppr;
+    const int64_t src = rows_idx ? (int64_t)rows_idx[r] : (int64_t)r;
+    u32x4 h;
+    if (src >= src_rows) {
+      const uint32_t nan2 = SDT == DT_BF16 ? 0x7fc07fc0u : 0x7e007e00u;
+      h = u32x4{nan2, nan2, nan2, nan2};
+    } else {
+      // bits [qq*8*BITS, (qq+1)*8*BITS) of the pack
+      const uint32_t* pw = w + src * P + (int64_t)p * BITS;
+      const uint32_t bit0 = qq * 8u * BITS;
+      const uint32_t i0 = bit0 >> 5, off = bit0 & 31u;
+      uint32_t e[8];
+      if constexpr (BITS == 4) {
+        const uint32_t v = pw[qq];
+#pragma unroll
+        for (int j = 0; j < 8; j++) e[j] = (v >> (4 * j)) & 0xfu;
+      } else if constexpr (BITS == 8) {
+        const uint32_t v0 = pw[2 * qq], v1 = pw[2 * qq + 1];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          e[j] = (v0 >> (8 * j)) & 0xffu;
+          e[j + 4] = (v1 >> (8 * j)) & 0xffu;
+        }
+      } else if constexpr (BITS == 2) {
+        const uint32_t v = pw[qq >> 1] >> (16u * (qq & 1u));
+#pragma unroll
+        for (int j = 0; j < 8; j++) e[j] = (v >> (2 * j)) & 0x3u;
+      } else {
+        const uint32_t i1 = i0 + 1 < (uint32_t)BITS ? i0 + 1 : i0;
+        const uint64_t v = ((uint64_t)pw[i1] << 32 | pw[i0]) >> off;
+#pragma unroll
+        for (int j = 0; j < 8; j++) e[j] = (uint32_t)(v >> (BITS * j)) & ((1u << BITS) - 1u);
+      }
+      const int64_t gi = src * G + (p >> gshift_packs);
+      const float sv = DT_<SDT>::to_f32(s[gi]), bv = DT_<SDT>::to_f32(b[gi]);
+      if (__builtin_isfinite(sv) && __builtin_isfinite(bv)) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) h[i] = deq_pair<SDT, false>(e[2 * i], e[2 * i + 1], sv, bv);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) h[i] = deq_pair<SDT, true>(e[2 * i], e[2 * i + 1], sv, bv);
+      }
+    }
+    *reinterpret_cast<u32x4*>(out + (int64_t)r * K + (int64_t)p * 32 + qq * 8) = h;
+  }
+}
+
 #define HQ_CAT_(a, b) a##b
 #define HQ_CAT(a, b) HQ_CAT_(a, b)
 
@@ -145,15 +210,21 @@ hipError_t HQ_CAT(launch_dequant_b, HQ_BITS)(const DeqArgs& a) {
           a.src_rows, gsp);
       break;
     case DT_F16:
-      dequant_kernel<HQ_BITS, DT_F16><<<blocks, 256, 0, a.stream>>>(
-          (uint16_t*)a.out, a.w, (const uint16_t*)a.s, (const uint16_t*)a.b, a.rows_idx, (uint32_t)total,
-          ppr, a.src_rows, gsp);
+    default: {
+      // quarter packs: 4 threads per pack (total < 2^31 / 32 * 4, checked by the caller)
+      const uint64_t tq = total * 4;
+      uint32_t qb = (uint32_t)((tq + 255) / 256);
+      if (qb > 65536u * 8u) qb = 65536u * 8u;
+      if (a.sdt == DT_F16)
+        dequant8_kernel<HQ_BITS, DT_F16><<<qb, 256, 0, a.stream>>>(
+            (uint16_t*)a.out, a.w, (const uint16_t*)a.s, (const uint16_t*)a.b, a.rows_idx,
+            (uint32_t)tq, ppr, a.src_rows, gsp);
+      else
+        dequant8_kernel<HQ_BITS, DT_BF16><<<qb, 256, 0, a.stream>>>(
+            (uint16_t*)a.out, a.w, (const uint16_t*)a.s, (const uint16_t*)a.b, a.rows_idx,
+            (uint32_t)tq, ppr, a.src_rows, gsp);
       break;
-    default:
-      dequant_kernel<HQ_BITS, DT_BF16><<<blocks, 256, 0, a.stream>>>(
-          (uint16_t*)a.out, a.w, (const uint16_t*)a.s, (const uint16_t*)a.b, a.rows_idx, (uint32_t)total,
-          ppr, a.src_rows, gsp);
-      break;
+    }
   }
   return hipGetLastError();
 }

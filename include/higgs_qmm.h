@@ -127,6 +127,7 @@ int hq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
  * qwen3_next.rs:308-318).
  *
  *   w: [rows, K*bits/32]; scales/biases: [rows, K/group_size]; out: [rows, K].
+ *   rows * K < 2^34 (HQ_ERR_INVALID_ARGUMENT otherwise).
  *
  * Rounding: for 16-bit scales each element is round(round(q*s) + b) -- the
  * product and the sum each rounded to s_dtype (round-to-nearest-even), as
