@@ -32,6 +32,27 @@ def test_exports_every_header_symbol():
     assert set(_lib.SIGNATURES) == syms
 
 
+def test_per_width_code_is_not_shared_between_widths():
+    """Each kernel source is compiled once per bit width; any symbol those
+    builds share (weak, merged by the linker) must carry the width as its
+    first template argument, or one width's code would serve all of them."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-C", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    shared = [ln.split(" ", 2)[2] for ln in out.splitlines()
+              if len(ln.split(" ", 2)) == 3 and ln.split(" ", 2)[1] in ("W", "V")
+              and "hq::" in ln]
+    assert shared, "expected the per-width kernel instantiations"
+    pat = re.compile(r"^void hq::(?:__device_stub__)?\w+_kernel<[2-8], ")
+    bad = [sym for sym in shared if not pat.match(sym)]
+    assert not bad, bad[:10]
+
+
 def test_version_and_result_dtype():
     assert "gfx950" in _lib.version()
     L = _lib.lib()
