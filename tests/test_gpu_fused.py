@@ -55,12 +55,13 @@ def test_dense_hidden_fused_matches_oracle(dev, M, bits, g):
     assert rel_err(to_host_f64(h), ref) <= 1e-2
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8])
 @pytest.mark.parametrize("K", [3072, 4096, 12288])
 @pytest.mark.parametrize("bits,g", [(4, 64), (4, 32), (8, 128)])
 def test_dense_hidden_fused_streaming(dev, M, K, bits, g):
-    # K a multiple of 1024 above 2048 at M <= 2: the streaming kernel with the
-    # gate and up halves in one block; N = 200 leaves a partial 16-row tile.
+    # K a multiple of 1024 above 2048: the streaming kernel with the gate and
+    # up halves in one block (M = 1, 2; M = 4, 8 at K <= 4096), the persistent
+    # kernel otherwise; N = 200 leaves a partial 16-row tile.
     N, dt = 200, O.BF16
     x, w, s, b = _dense_case(K + M * 10 + bits, M, N, K, bits, g, dt)
     h = ops.dense_hidden_fused(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
