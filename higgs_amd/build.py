@@ -27,9 +27,9 @@ BITS = (2, 3, 4, 5, 6, 8)
 PER_BITS = ("hq_dequant.hip", "hq_qmv.hip", "hq_qmvx.hip", "hq_qmm.hip")
 ONCE = ("hq_capi.hip", "hq_moe.hip")
 
-# -packed-fp32-ops off: hipcc must not form v_pk_{add,mul,fma}_f32 (see
-# DESIGN.md, hardware notes). Denormals are kept so fp16/fp32 dequantize
-# matches IEEE arithmetic bit for bit.
+# -packed-fp32-ops off: hipcc must not form packed fp32 add/mul/fma, whose
+# forms have given sporadic wrong results on these GPUs. Denormals are kept
+# so fp16/fp32 dequantize matches IEEE arithmetic bit for bit.
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
