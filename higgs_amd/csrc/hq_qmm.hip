@@ -683,12 +683,21 @@ __device__ __forceinline__ int64_t wave_lower_bound(const uint32_t* v, int64_t n
 // columns of the up projection; wave wn's fragment 0 holds gate columns
 // n0 + wn*16 .. + 15 and fragment 1 the matching up columns, so the epilogue
 // writes swiglu(gate, up) from registers.
-template <int BITS, int CT, int GS, bool SWI>
+template <int BITS, int CT, int GS, bool SWI, bool OCC>
 __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
+  // OCC (short K loops): 48 x rows, 144-byte LDS rows and a 2-deep ring,
+  // 50.7 KB of LDS and under 168 VGPRs, so three blocks fit a CU (configs[4]
+  // down, K = 768: 77 -> 73 us); with K = 2048 the shallow ring costs more
+  // than the occupancy gains (gate 77 -> 89 us), so longer K keeps 64 x rows,
+  // 160-byte rows and 4 steps of prefetch.
+  constexpr int XM = OCC ? 48 : QBM;
+  constexpr int LD = OCC ? GBK + 8 : GLD;
+  constexpr int RD = OCC ? 2 : kGD;
+  constexpr int NJX = XM / 16;
   using T = Mma<CT>;
   using ST = st_t<CT>;
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][QBN * GLD];  // W (dequantized)
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][QBM * GLD];  // x rows
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][QBN * LD];  // W (dequantized)
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][XM * LD];  // x rows
   __shared__ int64_t run[2];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -715,10 +724,12 @@ __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
   const int64_t P = (int64_t)(K >> 5) * BITS;
   const int64_t G = K / GS;
   const ST* xg = (const ST*)a.x;
-  const int wn = wv;  // wave owns W rows wn*32.. (2 fragments), all 64 x rows
+  const int wn = wv;  // wave owns W rows wn*32.. (2 fragments), all XM x rows
 
-  // x tile (64 x 64): thread copies chunks xc and xc + 4 of row xr.
-  const int xr = tid >> 2, xc = tid & 3;
+  // x tile (XM x 64): thread copies chunks xc and xc + 4 of row xr.
+  // (with XM < 64, threads past row XM - 1 repeat that row's loads and
+  // stores -- the same values -- so every thread runs the same code)
+  const int xr = min(tid >> 2, XM - 1), xc = tid & 3;
   // W tile (128 x 64): thread dequantizes pack wp of row wr. SWI: row wr is
   // column n0 + (wr / 32) * 16 + wr % 16 of the gate (bit 4 of wr clear) or
   // of the up projection.
@@ -743,76 +754,76 @@ __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
     p.bv = DT_<CT>::load(brow, gi);
   };
   auto wstore = [&](const WPre& p, int buf) {
-    uint16_t* dst = As[buf] + wr * GLD + wp * 32;
+    uint16_t* dst = As[buf] + wr * LD + wp * 32;
 #pragma unroll
     for (int qq = 0; qq < 4; qq++) *reinterpret_cast<u32x4*>(dst + qq * 8) = deq8<BITS, CT>(p.wd, qq, p.sv, p.bv);
   };
 
-  for (int64_t r0 = r_begin; r0 < r_end; r0 += QBM) {
+  for (int64_t r0 = r_begin; r0 < r_end; r0 += XM) {
     // this thread's x row: flattened row r -> batch element r / M, row r % M
     const int64_t r = min(r0 + xr, r_end - 1);
     const int64_t bi = r / M;
     const int64_t xi = a.lhs ? (int64_t)a.lhs[bi] : bi / a.x_rep;
     const ST* xrow = xg + (min(xi, a.x_batch - 1) * M + (r - bi * M)) * (int64_t)K + xc * 8;
 
-    floatx4 acc[2][4];
+    floatx4 acc[2][NJX];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NJX; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // Register ring of kGD steps: the loads of step kt + kGD are issued at
-    // step kt and land in LDS at step kt + kGD - 1, so kGD - 1 steps of
+    // Register ring of RD steps: the loads of step kt + RD are issued at
+    // step kt and land in LDS at step kt + RD - 1, so RD - 1 steps of
     // compute cover their latency. The ring index is a compile-time constant
     // inside the unrolled group, so no register copies force early waits.
     const int nk = K / GBK;
-    WPre wr_[kGD];
-    u32x4 xr_[kGD][2];
+    WPre wr_[RD];
+    u32x4 xr_[RD][2];
     auto xload_to = [&](u32x4 (&d)[2], int k0) {
       d[0] = *reinterpret_cast<const u32x4*>(xrow + k0);
       d[1] = *reinterpret_cast<const u32x4*>(xrow + k0 + 32);
     };
     auto xstore_from = [&](const u32x4 (&d)[2], int buf) {
-      *reinterpret_cast<u32x4*>(Bs[buf] + xr * GLD + xc * 8) = d[0];
-      *reinterpret_cast<u32x4*>(Bs[buf] + xr * GLD + xc * 8 + 32) = d[1];
+      *reinterpret_cast<u32x4*>(Bs[buf] + xr * LD + xc * 8) = d[0];
+      *reinterpret_cast<u32x4*>(Bs[buf] + xr * LD + xc * 8 + 32) = d[1];
     };
 #pragma unroll
-    for (int d = 0; d < kGD; d++) {
+    for (int d = 0; d < RD; d++) {
       xload_to(xr_[d], min(d, nk - 1) * GBK);
       wload(wr_[d], min(d, nk - 1) * GBK);
     }
     wstore(wr_[0], 0);
     xstore_from(xr_[0], 0);
     __syncthreads();
-    for (int kt0 = 0; kt0 < nk; kt0 += kGD) {
+    for (int kt0 = 0; kt0 < nk; kt0 += RD) {
 #pragma unroll
-      for (int d = 0; d < kGD; d++) {
+      for (int d = 0; d < RD; d++) {
         const int kt = kt0 + d;
         if (kt < nk) {
-          const int buf = d & 1;  // kGD is even, so kt & 1 == d & 1
+          const int buf = d & 1;  // RD is even, so kt & 1 == d & 1
 #pragma unroll
           for (int ks = 0; ks < GBK / 32; ks++) {
             const int kofs = ks * 32 + (lane >> 4) * 8;
-            typename T::frag fb[4];
+            typename T::frag fb[NJX];
 #pragma unroll
-            for (int j = 0; j < 4; j++)
+            for (int j = 0; j < NJX; j++)
               fb[j] = __builtin_bit_cast(typename T::frag, *reinterpret_cast<const u32x4*>(
-                                                               Bs[buf] + (j * 16 + (lane & 15)) * GLD + kofs));
+                                                               Bs[buf] + (j * 16 + (lane & 15)) * LD + kofs));
 #pragma unroll
             for (int i = 0; i < 2; i++) {
               const typename T::frag fa = __builtin_bit_cast(
                   typename T::frag,
-                  *reinterpret_cast<const u32x4*>(As[buf] + (wn * 32 + i * 16 + (lane & 15)) * GLD + kofs));
+                  *reinterpret_cast<const u32x4*>(As[buf] + (wn * 32 + i * 16 + (lane & 15)) * LD + kofs));
 #pragma unroll
-              for (int j = 0; j < 4; j++) acc[i][j] = T::mma(fa, fb[j], acc[i][j]);
+              for (int j = 0; j < NJX; j++) acc[i][j] = T::mma(fa, fb[j], acc[i][j]);
             }
           }
           // step kt + 1 (ring slot d + 1) into the other buffer; refill slot d
-          // with step kt + kGD (past the end: reload the last step, unused)
-          wstore(wr_[(d + 1) % kGD], buf ^ 1);
-          xstore_from(xr_[(d + 1) % kGD], buf ^ 1);
-          xload_to(xr_[d], min(kt + kGD, nk - 1) * GBK);
-          wload(wr_[d], min(kt + kGD, nk - 1) * GBK);
+          // with step kt + RD (past the end: reload the last step, unused)
+          wstore(wr_[(d + 1) % RD], buf ^ 1);
+          xstore_from(xr_[(d + 1) % RD], buf ^ 1);
+          xload_to(xr_[d], min(kt + RD, nk - 1) * GBK);
+          wload(wr_[d], min(kt + RD, nk - 1) * GBK);
           __syncthreads();
         }
       }
@@ -822,7 +833,7 @@ __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
     // (SWI: acc[0] gate and acc[1] up of column n0 + wn*16 + 4*(lane>>4) + v)
     if constexpr (SWI) {
 #pragma unroll
-      for (int j = 0; j < 4; j++)
+      for (int j = 0; j < NJX; j++)
 #pragma unroll
         for (int v = 0; v < 4; v++)
           acc[0][j][v] = swiglu_f32(DT_<CT>::round(acc[0][j][v]), DT_<CT>::round(acc[1][j][v]));
@@ -831,7 +842,7 @@ __global__ __launch_bounds__(256) void gqmm_kernel(GQKern a) {
     for (int i = 0; i < (SWI ? 1 : 2); i++) {
       const int n = n0 + wn * (SWI ? 16 : 32) + i * 16 + 4 * (lane >> 4);
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < NJX; j++) {
         const int64_t rr = r0 + j * 16 + (lane & 15);
         if (rr >= r_end) continue;
         const int64_t rb = rr / M;
@@ -865,7 +876,10 @@ hipError_t run_gqmm(const QArgs& a) {
   k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
   const int ont = SWI ? QBN / 2 : QBN;
   dim3 grid((unsigned)((a.N + ont - 1) / ont), (unsigned)(a.w_batch + 1));
-  hipLaunchKernelGGL((gqmm_kernel<HQ_BITS, CT, GS, SWI>), grid, dim3(256), 0, a.stream, k);
+  if (a.K <= 1024)
+    hipLaunchKernelGGL((gqmm_kernel<HQ_BITS, CT, GS, SWI, true>), grid, dim3(256), 0, a.stream, k);
+  else
+    hipLaunchKernelGGL((gqmm_kernel<HQ_BITS, CT, GS, SWI, false>), grid, dim3(256), 0, a.stream, k);
   return hipGetLastError();
 }
 
