@@ -639,7 +639,8 @@ hipError_t run_qgemm_g(const QArgs& a) {
 // by its W tile -- each expert's weights stream from HBM once per 64 rows.
 // The extra block row e == w_batch fills the rows of out-of-range indices
 // (sorted to the end) with NaN. Same LDS-dequant MFMA pipeline as the
-// large-tile GEMM, at a 128 x 64 tile with 4 waves (2 blocks per CU).
+// large-tile GEMM, at a 128 x 64 tile with 4 waves (2 blocks per CU), or
+// 128 x 48 with 3 blocks per CU for K <= 1024.
 // ---------------------------------------------------------------------------
 constexpr int QBN = 128, QBM = 64;
 constexpr int kGD = 4;  // register prefetch depth (K-steps) of the grouped kernel
