@@ -1179,15 +1179,15 @@ hipError_t run_qmvx(const QArgs& a) {
   return hipGetLastError();
 }
 
-// One or two rows of x, x and scales of one 16-bit type, K a multiple of 1024
-// above 2048: the streaming kernel, one K range per wave when K <= 8192 (two
-// when K <= 16384), one tile per block (two for vocabulary-sized N at
-// M = 1). Measured at M = 1 on the Llama-3-8B decode shapes (4-bit g64,
-// graph of distinct weight copies) against the persistent kernel below:
-// 4096 x 4096 4.66 vs 5.03 us, 14336 x 4096 8.77 vs 9.82 us, 128256 x 4096
-// 54.8 vs 68.9 us; at K = 2048 the persistent kernel stays (8192 x 2048:
-// 4.67 vs 4.90 us). At M = 2 the whole Llama-3-8B step (225 launches) takes
-// 1.63 ms here against 1.91 ms on the persistent kernel.
+// x and scales of one 16-bit type, K a multiple of 1024 above 2048, one or
+// two rows of x (four or eight at K <= 4096): the streaming kernel, one K
+// range per wave (two 1024-element ranges per wave above K = 8192), one tile
+// per block (two for vocabulary-sized N at M = 1). Measured at M = 1 on the
+// Llama-3-8B decode shapes (4-bit g64, graph of distinct weight copies)
+// against the persistent kernel below, with 1024-element ranges: 4096 x 4096
+// 4.66 vs 5.03 us, 14336 x 4096 8.77 vs 9.82 us, 128256 x 4096 54.8 vs
+// 68.9 us; at K = 2048 the persistent kernel stays (8192 x 2048: 4.67 vs
+// 4.90 us).
 template <int XDT, int GS, int MB, bool SWI>
 hipError_t run_qmvs_auto(const QArgs& a) {
   // Llama-3-8B step: B = 2 1.53 ms (1.63 with 1024-element ranges, 1.91 on
