@@ -290,8 +290,11 @@ def bench_moe(dev, steps):
                 ops.gather_qmm(xs, w, s, b, None, srt, True, GROUP, BITS, True)
         ms = time_graph(run, steps, 1, dev) / len(ws)
         byts = used * (N * K // 2 + 2 * N * (K // GROUP) * 2) + 2 * T * TK * (K + N)
+        gbs = byts / (ms * 1e-3) / 1e9
+        # HBM-bound at configs[4] (arithmetic intensity ~94 FLOP/B < ridge
+        # ~312): achieved = ideal time (bytes / 8 TB/s) / measured time
         out[name] = {"rows": T * TK, "experts": E, "N": N, "K": K, "us": round(ms * 1e3, 2),
-                     "GB/s": round(byts / (ms * 1e-3) / 1e9, 1)}
+                     "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         del ws
     # the whole expert block (qwen3_moe.rs:353-357 around forward_gather_global_sort)
     blocks = [tuple(gen.torch_quantized(80 + 3 * c + j, *nk, BITS, GROUP, dev, lead=(E,))
@@ -308,7 +311,8 @@ def bench_moe(dev, steps):
         T * TK * 2 * (H + I + I + H)
     out["block"] = {"tokens": T, "top_k": TK, "experts": E, "hidden": H, "intermediate": I,
                     "launches": 4, "us": round(ms * 1e3, 2),
-                    "GB/s": round(byts / (ms * 1e-3) / 1e9, 1)}
+                    "GB/s": round(byts / (ms * 1e-3) / 1e9, 1),
+                    "frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del blocks
     torch.cuda.empty_cache()
     return out
