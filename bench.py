@@ -16,8 +16,8 @@ Printed JSON line (one, on stdout):
                 stream around the timed replays; peak = MI355X HBM3E 8 TB/s. `traffic` is the measured
                 HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
                 WRITE_SIZE summary (profiles/), or null if absent.
-  qmv_shapes    per-projection mean launch time and GB/s (graph of the 32
-                distinct layer copies of that projection)
+  qmv_shapes    per-projection mean launch time and GB/s (one graph over
+                >= 1 GiB of distinct copies of that projection)
   qmv_batch     the decode step at B = 1, 4, 8
   qmm           configs[2]: M = 2048 prefill GEMMs, TFLOP/s and fraction of
                 the 2.5 PFLOP/s dense bf16 MFMA peak
@@ -34,13 +34,20 @@ Printed JSON line (one, on stdout):
                 concatenated (one launch), gate/up + SwiGLU in one launch
                 (hq_quantized_matmul_swiglu, the reference's
                 dense_hidden_fused), o, down, lm_head: 129 launches
-  cpu_baseline  the CPU oracle's MLX-style quantized_matmul on the host cores,
-                on a bounded sample of the same workload (layer 0's seven
-                projections at B)
+  cpu_baseline  the CPU oracle's MLX-style quantized_matmul on every host
+                CPU the job may run on (and on 1 thread), on a bounded sample
+                of the same workload (layer 0's seven projections at B), with
+                the CPU model and counts
+
+Every timed graph cycles through >= 1 GiB of distinct weights (4x the 256 MB
+Infinity Cache), so weights stream from HBM in every section.
 
 Other modes (for profiling runs):
   --mode copy   a plain device copy of --copy-mb MB (calibrates rocprofv3
                 FETCH_SIZE / WRITE_SIZE against known bytes)
+  --mode launch the per-launch floor: a graph of 225 launches of the
+                library's smallest kernel
+  --only S,...  run only the named extra sections (no headline, no CPU leg)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
 """
@@ -175,19 +182,43 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
+ROTATE_BYTES = 1 << 30  # distinct weight bytes a timed graph cycles through (4x the MALL)
+
+
+def rotation(N, K, bits=BITS, g=GROUP, have=0, lead=1):
+    """Copies of a [lead, N, K] quantized matrix needed for >= ROTATE_BYTES of
+    distinct weights (packed words + scales + biases); `have` copies exist."""
+    wb = lead * (N * K * bits // 8 + 2 * N * (K // g) * 2)
+    return max(have, -(-ROTATE_BYTES // wb))
+
+
 def bench_shapes(model, B, dev, steps):
+    """Per projection: one graph over >= 1 GiB of distinct copies of that
+    projection (the model's 32 layer copies plus extra ones), so the 256 MB
+    Infinity Cache cannot serve the weights."""
+    import torch
+
+    from higgs_amd import gen
+
     out = {}
     for name, N, K in LAYER_SHAPES + [("lm_head", VOCAB, HIDDEN)]:
-        p = Plan(model.calls(only=name), B, dev)
+        calls = list(model.calls(only=name))
+        for c in range(rotation(N, K, have=len(calls)) - len(calls)):
+            calls.append((name, gen.torch_quantized(20000 + 64 * c + len(name), N, K, BITS, GROUP,
+                                                    dev), N, K))
+        p = Plan(calls, B, dev)
         ms = time_graph(p.run, steps, 2, dev)
         n = len(p.plan)
         out[name] = {"N": N, "K": K, "us_per_launch": round(ms * 1e3 / n, 3),
-                     "GB/s": round(p.bytes / (ms * 1e-3) / 1e9, 1)}
+                     "GB/s": round(p.bytes / (ms * 1e-3) / 1e9, 1), "copies": n,
+                     "distinct_MB": round(n * (N * K // 2 + 2 * N * (K // GROUP) * 2) / 1e6)}
+        del calls, p
+        torch.cuda.empty_cache()
     return out
 
 
 def bench_qmm(model, dev, steps):
-    """M=2048 prefill GEMMs over layer 0..3 gate and down weights."""
+    """M=2048 prefill GEMMs over the 32 layers' gate and down weights."""
     import torch
 
     from higgs_amd import _lib, gen
@@ -195,7 +226,8 @@ def bench_qmm(model, dev, steps):
     lib = _lib.lib()
     out = {}
     for name, N, K in (("gate_up", INTER, HIDDEN), ("down", HIDDEN, INTER)):
-        ws = [model.layers[l]["gate" if name == "gate_up" else "down"] for l in range(4)]
+        # all 32 layer copies: 1.06 GB of distinct weights per replay
+        ws = [model.layers[l]["gate" if name == "gate_up" else "down"] for l in range(LAYERS)]
         x = gen.torch_x(3, (2048, K), dev)
         y = torch.empty((2048, N), dtype=torch.bfloat16, device=dev)
 
@@ -282,7 +314,9 @@ def bench_moe(dev, steps):
     used = len(np.unique(idx))
     out = {}
     for name, N, K in (("gate", I, H), ("down", H, I)):
-        ws = [gen.torch_quantized(70 + c, N, K, BITS, GROUP, dev, lead=(E,)) for c in range(3)]
+        # >= 1 GiB of distinct expert weights per replay (10 copies of 113 MB)
+        ws = [gen.torch_quantized(70 + c, N, K, BITS, GROUP, dev, lead=(E,))
+              for c in range(rotation(N, K, lead=E))]
         xs = gen.torch_x(71, (T, K), dev)[tok].reshape(-1, 1, K).contiguous()
 
         def run(stream, ws=ws, xs=xs):
@@ -297,8 +331,9 @@ def bench_moe(dev, steps):
                      "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         del ws
     # the whole expert block (qwen3_moe.rs:353-357 around forward_gather_global_sort)
+    # 4 copies of the block's gate, up and down experts: 1.36 GB distinct
     blocks = [tuple(gen.torch_quantized(80 + 3 * c + j, *nk, BITS, GROUP, dev, lead=(E,))
-                    for j, nk in enumerate(((I, H), (I, H), (H, I)))) for c in range(3)]
+                    for j, nk in enumerate(((I, H), (I, H), (H, I)))) for c in range(4)]
     x = gen.torch_x(72, (1, T, H), dev)
     idx_d = torch.from_numpy(idx.astype(np.int32)).to(dev).reshape(1, T, TK)
     sc = torch.softmax(gen.torch_x(73, (1, T, TK), dev).float(), -1).to(torch.bfloat16)
@@ -388,8 +423,9 @@ def bench_dequant(dev, steps):
                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
         del ws
 
-    whole("c0_8192x2048", 8192, 2048, 32)
-    whole("gate_14336x4096", 14336, 4096, 8)
+    # >= 1 GiB of distinct packed weights + scales/biases per replay
+    whole("c0_8192x2048", 8192, 2048, rotation(8192, 2048))
+    whole("gate_14336x4096", 14336, 4096, rotation(14336, 4096))
     # embedding: 32 batches of 512 token ids into a [128256, 4096] table (one
     # graph of 32 launches: a single small launch per replay would time the
     # host's graph launch instead)
@@ -413,9 +449,47 @@ def bench_dequant(dev, steps):
     return out
 
 
+def host_cpus():
+    """(threads to use, description) for the CPU baseline: every CPU this process
+    may run on -- its affinity mask, capped by a cgroup CPU quota when one is
+    set -- plus the host's CPU model and counts."""
+    import re as _re
+
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    quota = None
+    for path in ("/sys/fs/cgroup/cpu.max", "/sys/fs/cgroup/cpu/cpu.cfs_quota_us"):
+        try:
+            txt = open(path).read().split()
+        except OSError:
+            continue
+        try:
+            if path.endswith("cpu.max") and txt[0] != "max":
+                quota = int(txt[0]) / int(txt[1])
+            elif not path.endswith("cpu.max") and int(txt[0]) > 0:
+                period = int(open("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read())
+                quota = int(txt[0]) / period
+        except (OSError, ValueError, IndexError):
+            quota = None
+        break
+    threads = affinity if quota is None else max(1, min(affinity, int(quota)))
+    try:
+        models = _re.findall(r"^model name\s*:\s*(.*)$", open("/proc/cpuinfo").read(), _re.M)
+    except OSError:
+        models = []
+    info = {"cpu_model": models[0].strip() if models else "unknown",
+            "nproc": os.cpu_count(), "affinity_cpus": affinity,
+            "cgroup_cpu_quota": None if quota is None else round(quota, 2),
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+    return threads, info
+
+
 def cpu_baseline(model, B, target_s):
     """Oracle quantized_matmul (MLX-CPU-style restatement, oracle/hq_oracle.c
-    hqo_qmm_mlx) on the host, over layer 0's seven projections at batch B."""
+    hqo_qmm_mlx) on the host, over layer 0's seven projections at batch B:
+    on every CPU the job may use, and on one thread."""
     import numpy as np
     import torch
 
@@ -437,7 +511,7 @@ def cpu_baseline(model, B, target_s):
             O.qmm_mlx(x, O.BF16, w, s, b, O.BF16, GROUP, BITS, threads=threads)
 
     res = {}
-    threads_all = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    threads_all, info = host_cpus()
     for threads in (1, threads_all):
         t0 = time.perf_counter()
         one_pass(threads)
@@ -449,12 +523,14 @@ def cpu_baseline(model, B, target_s):
         dt = (time.perf_counter() - t0) / reps
         res[threads] = (nbytes / dt / 1e9, reps)
     gbs_all, reps_all = res[threads_all]
-    return {"value": round(gbs_all, 3), "unit": "GB/s", "cores": threads_all, "kind": "port",
-            "value_1thread": round(res[1][0], 3),
-            "sample": f"Llama-3-8B layer 0 q,k,v,o,gate,up,down at B={B} "
-                      f"({nbytes / 1e6:.1f} MB algorithmic), {reps_all} passes at "
-                      f"{threads_all} threads and {res[1][1]} at 1 thread, oracle hqo_qmm_mlx "
-                      f"(float lanes, MLX CPU loop order)"}
+    out = {"value": round(gbs_all, 3), "unit": "GB/s", "cores": threads_all, "kind": "port",
+           "value_1thread": round(res[1][0], 3),
+           "sample": f"Llama-3-8B layer 0 q,k,v,o,gate,up,down at B={B} "
+                     f"({nbytes / 1e6:.1f} MB algorithmic), {reps_all} passes on "
+                     f"{threads_all} threads (every CPU the job may use) and {res[1][1]} on "
+                     f"1 thread, oracle hqo_qmm_mlx (float lanes, MLX CPU loop order)"}
+    out.update(info)
+    return out
 
 
 def mode_copy(dev, mb, steps):
@@ -473,6 +549,70 @@ def mode_copy(dev, mb, steps):
                       "ms": round(dt * 1e3, 4), "GB/s": round(8 * n / dt / 1e9, 1)}), flush=True)
 
 
+def bench_batch(model, args, step, dev):
+    qb = {}
+    for B in (1, 4, 8):
+        st = step if (step is not None and B == args.batch) else Plan(model.calls(), B, dev)
+        m = time_graph(st.run, max(5, args.steps // 2), 2, dev)
+        qb[str(B)] = {"ms_per_step": round(m, 4), "GB/s": round(st.bytes / (m * 1e-3) / 1e9, 1),
+                      "frac": round(st.bytes / (m * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return qb
+
+
+def bench_fused(model, args, dev):
+    import torch
+
+    fp = FusedPlan(model, args.batch, dev)
+    mf = time_graph(fp.run, args.steps, 2, dev)
+    r = {"batch": args.batch, "launches": len(fp.calls), "ms_per_step": round(mf, 4),
+         "GB/s": round(fp.bytes / (mf * 1e-3) / 1e9, 1),
+         "frac": round(fp.bytes / (mf * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+         "tokens_per_s": round(1e3 / mf, 1)}
+    del fp
+    torch.cuda.empty_cache()
+    return r
+
+
+SECTIONS = ("qmv_shapes", "qmv_batch", "qmm", "moe", "configs", "dequant", "decode_fused")
+
+
+def sections(model, args, step, dev):
+    """(name, thunk) of the extra sections, in output order (all, or --only's)."""
+    sub = max(3, args.steps // 4)
+    table = {
+        "qmv_shapes": lambda: bench_shapes(model, args.batch, dev, sub),
+        "qmv_batch": lambda: bench_batch(model, args, step, dev),
+        "qmm": lambda: bench_qmm(model, dev, sub),
+        "moe": lambda: bench_moe(dev, sub),
+        "configs": lambda: bench_configs(dev, sub),
+        "dequant": lambda: bench_dequant(dev, sub),
+        "decode_fused": lambda: bench_fused(model, args, dev),
+    }
+    names = SECTIONS if not args.only else args.only.split(",")
+    return [(n, table[n]) for n in names]
+
+
+def mode_launch(dev, steps, launches=225):
+    """Per-launch floor: a graph of `launches` launches of this library's
+    smallest kernel (hq_swiglu over 64 elements, one block), timed like the
+    decode step. It is the cost every launch of the step pays before any
+    weight byte moves."""
+    import torch
+
+    from higgs_amd import _lib
+
+    lib = _lib.lib()
+    g = torch.zeros(64, dtype=torch.bfloat16, device=dev)
+    o = torch.empty_like(g)
+
+    def run(stream):
+        for _ in range(launches):
+            _lib.check(lib.hq_swiglu(o.data_ptr(), g.data_ptr(), g.data_ptr(), 64, 2, stream))
+    ms = time_graph(run, steps, 3, dev)
+    print(json.dumps({"mode": "launch", "launches": launches, "ms_per_graph": round(ms, 4),
+                      "us_per_launch": round(ms * 1e3 / launches, 3)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -483,9 +623,16 @@ def main():
                     help="target seconds per CPU thread-count leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip shapes, batch, qmm, moe")
-    ap.add_argument("--mode", default="decode", choices=("decode", "copy"))
+    ap.add_argument("--mode", default="decode", choices=("decode", "copy", "launch"))
     ap.add_argument("--copy-mb", type=int, default=512)
+    ap.add_argument("--only", default="",
+                    help="comma-separated extra sections to run alone, without the headline step "
+                         "or the CPU baseline (profiling runs); prints one JSON object of them: "
+                         + ", ".join(SECTIONS))
     args = ap.parse_args()
+    for n in filter(None, args.only.split(",")):
+        if n not in SECTIONS:
+            ap.error(f"--only: unknown section {n!r} (choose from {', '.join(SECTIONS)})")
     if args.gpus != 1:
         print(f"bench.py measures one GPU (got --gpus {args.gpus}): this build's path is the "
               "single-GPU quantized-linear kernel set; multi-GPU sharding is design-only",
@@ -498,10 +645,22 @@ def main():
     if args.mode == "copy":
         mode_copy(dev, args.copy_mb, args.steps)
         return
+    if args.mode == "launch":
+        mode_launch(dev, args.steps)
+        return
 
     from higgs_amd import _lib
 
     log(f"[bench] {_lib.version()} on {torch.cuda.get_device_name(0)}")
+    if args.only:
+        needs_model = {"qmv_shapes", "qmv_batch", "qmm", "decode_fused"}
+        model = Model(dev) if needs_model & set(args.only.split(",")) else None
+        out = {}
+        for name, fn in sections(model, args, None, dev):
+            out[name] = fn()
+            log(f"[bench] {name}: {out[name]}")
+        print(json.dumps({"only": out}), flush=True)
+        return
     model = Model(dev)
     step = Plan(model.calls(), args.batch, dev)
     log(f"[bench] weights resident: {step.bytes / 1e9:.2f} GB algorithmic per step, "
@@ -516,32 +675,9 @@ def main():
 
     extras = {}
     if not args.no_extras:
-        extras["qmv_shapes"] = bench_shapes(model, args.batch, dev, max(3, args.steps // 4))
-        log(f"[bench] shapes: {extras['qmv_shapes']}")
-        qb = {}
-        for B in (1, 4, 8):
-            st = step if B == args.batch else Plan(model.calls(), B, dev)
-            m = time_graph(st.run, max(5, args.steps // 2), 2, dev)
-            qb[str(B)] = {"ms_per_step": round(m, 4), "GB/s": round(st.bytes / (m * 1e-3) / 1e9, 1)}
-        extras["qmv_batch"] = qb
-        log(f"[bench] batch sweep: {qb}")
-        extras["qmm"] = bench_qmm(model, dev, max(3, args.steps // 4))
-        log(f"[bench] qmm: {extras['qmm']}")
-        extras["moe"] = bench_moe(dev, max(3, args.steps // 4))
-        log(f"[bench] moe: {extras['moe']}")
-        extras["configs"] = bench_configs(dev, max(3, args.steps // 4))
-        log(f"[bench] configs: {extras['configs']}")
-        extras["dequant"] = bench_dequant(dev, max(3, args.steps // 4))
-        log(f"[bench] dequant: {extras['dequant']}")
-        fp = FusedPlan(model, args.batch, dev)
-        mf = time_graph(fp.run, args.steps, 2, dev)
-        extras["decode_fused"] = {"batch": args.batch, "launches": len(fp.calls),
-                                  "ms_per_step": round(mf, 4),
-                                  "GB/s": round(fp.bytes / (mf * 1e-3) / 1e9, 1),
-                                  "frac": round(fp.bytes / (mf * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                  "tokens_per_s": round(1e3 / mf, 1)}
-        log(f"[bench] fused decode step: {extras['decode_fused']}")
-        del fp
+        for name, fn in sections(model, args, step, dev):
+            extras[name] = fn()
+            log(f"[bench] {name}: {extras[name]}")
         torch.cuda.empty_cache()
 
     cpu = None

@@ -30,7 +30,10 @@ SIGNATURES = {
                                    _int, _int, _int, _vp]),
     "hq_gather_qmm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _int, _int, _int, _int, _int, _int, _vp]),
+    "hq_quantized_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int,
+                                   _int, _int, _int, _vp]),
     "hq_dequantize": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp]),
+    "hq_quantize": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _int, _vp]),
     "hq_embedding_dequantize": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int,
                                        _int, _vp]),
     "hq_quantized_matmul_swiglu": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,

@@ -25,7 +25,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 BITS = (2, 3, 4, 5, 6, 8)
 PER_BITS = ("hq_dequant.hip", "hq_qmv.hip", "hq_qmvx.hip", "hq_qmm.hip")
-ONCE = ("hq_capi.hip", "hq_moe.hip")
+ONCE = ("hq_capi.hip", "hq_moe.hip", "hq_quant.hip", "hq_device.hip")
 
 # -packed-fp32-ops off: hipcc must not form packed fp32 add/mul/fma, whose
 # forms have given sporadic wrong results on these GPUs. Denormals are kept

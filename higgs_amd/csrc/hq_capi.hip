@@ -127,10 +127,16 @@ int hq_result_dtype(int x_dtype, int s_dtype) {
   return x_dtype == s_dtype ? x_dtype : HQ_DTYPE_FLOAT32;
 }
 
-int hq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
-                        const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
-                        int group_size, int bits, int x_dtype, int s_dtype, void* stream) {
-  const char* tag = "quantized_matmul";
+}  // extern "C"
+
+namespace {
+
+// quantized_matmul with an optional linear-layer bias (lb, [N] of the output
+// dtype, transpose != 0 only).
+int quantized_matmul_impl(const char* tag, void* y, const void* x, const uint32_t* w,
+                          const void* scales, const void* biases, const void* lb, int64_t M,
+                          int64_t N, int64_t K, int transpose, int group_size, int bits,
+                          int x_dtype, int s_dtype, void* stream) {
   int rc = check_common(tag, group_size, bits, x_dtype, s_dtype);
   if (rc) return rc;
   if (M < 0 || N < 0 || K <= 0 || M > kMaxDim || N > kMaxDim || K > kMaxDim)
@@ -153,8 +159,40 @@ int hq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* s
   a.batch = 1; a.x_rep = 1; a.x_batch = 1; a.w_batch = 1;
   a.M = M; a.N = N; a.K = K;
   a.group_size = group_size; a.xdt = x_dtype; a.sdt = s_dtype; a.sorted = 0;
+  a.lb = lb;
   a.stream = (hipStream_t)stream;
   return run_q(tag, bits, a, transpose);
+}
+
+}  // namespace
+
+extern "C" {
+
+int hq_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
+                        int group_size, int bits, int x_dtype, int s_dtype, void* stream) {
+  return quantized_matmul_impl("quantized_matmul", y, x, w, scales, biases, nullptr, M, N, K,
+                               transpose, group_size, bits, x_dtype, s_dtype, stream);
+}
+
+int hq_quantized_linear(void* y, const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, const void* bias, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits, int x_dtype, int s_dtype, int bias_dtype,
+                        void* stream) {
+  const char* tag = "quantized_linear";
+  if (bias != nullptr) {
+    if (!dtype_ok(bias_dtype))
+      return fail(HQ_ERR_INVALID_ARGUMENT,
+                  "[%s] Only real floating types are supported but the bias has dtype code %d.",
+                  tag, bias_dtype);
+    if (dtype_ok(x_dtype) && dtype_ok(s_dtype) &&
+        bias_dtype != (x_dtype == s_dtype ? x_dtype : HQ_DTYPE_FLOAT32))
+      return fail(HQ_ERR_UNSUPPORTED,
+                  "[%s] The bias dtype (%d) must be the output dtype of the product (%d).", tag,
+                  bias_dtype, x_dtype == s_dtype ? x_dtype : HQ_DTYPE_FLOAT32);
+  }
+  return quantized_matmul_impl(tag, y, x, w, scales, biases, bias, M, N, K, 1, group_size, bits,
+                               x_dtype, s_dtype, stream);
 }
 
 int hq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
@@ -353,6 +391,39 @@ int hq_gather_qmm_swiglu(void* h, const void* x, const uint32_t* w_gate, const v
                 "== 0 and w_batch < 65535 (got dtypes %d, %d, K=%lld, w_batch=%lld).",
                 tag, x_dtype, s_dtype, (long long)K, (long long)w_batch);
   }
+  if (e != hipSuccess)
+    return fail(HQ_ERR_HIP, "[%s] kernel launch failed: %s", tag, hipGetErrorString(e));
+  return HQ_OK;
+}
+
+int hq_quantize(uint32_t* wq, void* scales, void* biases, const void* w, int64_t rows, int64_t K,
+                int group_size, int bits, int dtype, void* stream) {
+  const char* tag = "quantize";
+  int rc = check_common(tag, group_size, bits, -1, dtype);
+  if (rc) return rc;
+  if (rows < 0 || K <= 0 || K % group_size || rows > kMaxDim || K > kMaxDim ||
+      rows * K >= ((int64_t)1 << 40))
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] The last dimension of the matrix (%lld) must be divisible by the group size "
+                "%d (rows=%lld).",
+                tag, (long long)K, group_size, (long long)rows);
+  if (rows == 0) return HQ_OK;
+  if (!wq || !scales || !biases || !w)
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] NULL buffer pointer.", tag);
+  if (!aligned16(w) || (reinterpret_cast<uintptr_t>(wq) & 3u) ||
+      (reinterpret_cast<uintptr_t>(scales) & 1u) || (reinterpret_cast<uintptr_t>(biases) & 1u))
+    return fail(HQ_ERR_INVALID_ARGUMENT,
+                "[%s] w must be 16-byte aligned, wq 4-byte aligned, scales and biases aligned to "
+                "their dtype.", tag);
+  if (dtype == HQ_DTYPE_FLOAT32 &&
+      ((reinterpret_cast<uintptr_t>(scales) & 3u) || (reinterpret_cast<uintptr_t>(biases) & 3u)))
+    return fail(HQ_ERR_INVALID_ARGUMENT, "[%s] float32 scales and biases must be 4-byte aligned.",
+                tag);
+  hq::QuantArgs a{};
+  a.wq = wq; a.s = scales; a.b = biases; a.w = w;
+  a.rows = rows; a.K = K; a.group_size = group_size; a.bits = bits; a.dt = dtype;
+  a.stream = (hipStream_t)stream;
+  hipError_t e = hq::launch_quantize(a);
   if (e != hipSuccess)
     return fail(HQ_ERR_HIP, "[%s] kernel launch failed: %s", tag, hipGetErrorString(e));
   return HQ_OK;

@@ -79,6 +79,17 @@ __device__ __forceinline__ float swiglu_f32(float g, float u) {
   return g / (1.f + __expf(-g)) * u;
 }
 
+// One output element of a quantized linear layer: the product rounded to the
+// output dtype, then the layer's bias (`lbias`, [N] of the output dtype; null
+// for none) added and rounded again -- mlx-rs QuantizedLinear::forward is
+// quantized_matmul followed by an add (two roundings for 16-bit outputs).
+template <int ODT>
+__device__ __forceinline__ st_t<ODT> linear_out(float acc, const void* lbias, int64_t n) {
+  if (lbias != nullptr)
+    return DT_<ODT>::from_f32(DT_<ODT>::round(acc) + DT_<ODT>::load((const st_t<ODT>*)lbias, n));
+  return DT_<ODT>::from_f32(acc);
+}
+
 // Load 8 consecutive elements (16 B for 16-bit types, 32 B for float32) and
 // widen to float. `p` must be 16-B aligned for 16-bit types.
 template <int DT>

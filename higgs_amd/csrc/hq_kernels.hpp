@@ -35,6 +35,10 @@ struct QArgs {
   const uint32_t* w2;
   const void* s2;
   const void* b2;
+  // Bias of a quantized linear layer ([N] of the output dtype), added after
+  // the product is rounded (linear_out); null for none. One product only
+  // (batch == 1), never with the SwiGLU fusion.
+  const void* lb;
   hipStream_t stream;
 };
 
@@ -51,6 +55,19 @@ struct DeqArgs {
   int sdt;
   hipStream_t stream;
 };
+
+// Affine group quantization (hq_quant.hip): w [rows, K] of dt -> wq u32
+// [rows, K*bits/32], scales and biases [rows, K/group_size] of dt.
+struct QuantArgs {
+  uint32_t* wq;
+  void* s;
+  void* b;
+  const void* w;
+  int64_t rows, K;
+  int group_size, bits, dt;
+  hipStream_t stream;
+};
+hipError_t launch_quantize(const QuantArgs& a);
 
 #define HQ_DECLARE_LAUNCHERS(B)                          \
   hipError_t launch_dequant_b##B(const DeqArgs& a);      \

@@ -10,6 +10,7 @@
 //   crates/higgs-models/src/qwen3_moe.rs:355-357     y * scores, sum over top_k
 //   crates/higgs-models/src/qwen3_next.rs:340-342    swiglu(gate, up)
 #include "hq_common.hpp"
+#include "hq_device.hpp"
 #include "hq_moe.hpp"
 
 namespace hq {
@@ -215,12 +216,10 @@ size_t moe_sort_lds(int64_t E) {
 
 hipError_t launch_moe_sort(const SortArgs& a) {
   const size_t lds = moe_sort_lds(a.E);
-  static bool big = false;
-  if (lds > 64 * 1024 && !big) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_sort_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  static std::atomic<uint64_t> raised{0};
+  if (lds > 64 * 1024) {
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(moe_sort_kernel), 160 * 1024, raised);
     if (e != hipSuccess) return e;
-    big = true;
   }
   hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(kSortThreads), lds, a.stream, a);
   return hipGetLastError();

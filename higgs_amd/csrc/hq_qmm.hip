@@ -12,6 +12,7 @@
 // with fp32 accumulation. Gathered batches (gather_qmm with M > 8) use
 // blockIdx.z.
 #include "hq_common.hpp"
+#include "hq_device.hpp"
 #include "hq_kernels.hpp"
 
 #ifndef HQ_BITS
@@ -31,6 +32,7 @@ struct QKernM {
   int64_t batch, x_rep, x_batch, w_batch;
   int M, N, K;
   int gshift;
+  const void* lb;  // linear bias [N] or null
 };
 
 template <int CT> struct Mma;
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(256) void qmm_t_kernel(QKernM a) {
           const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
           if (gm < M && gn < N) {
             const float o = bad ? __uint_as_float(0x7fc00000u) : acc[i][j][v];
-            yb[(int64_t)gm * N + gn] = DT_<ODT>::from_f32(o);
+            yb[(int64_t)gm * N + gn] = linear_out<ODT>(o, a.lb, gn);
           }
         }
   }
@@ -254,6 +256,7 @@ struct GKern {
   const uint32_t* w2;  // SwiGLU up projection (gate is w/s/b), N rows
   const void* s2;
   const void* b2;
+  const void* lb;      // linear bias [N] or null (not with SwiGLU)
 };
 
 template <int CT>
@@ -530,6 +533,21 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
     }
     return;
   }
+  if (a.lb != nullptr) {
+    // linear bias: round the product, add the bias, round again
+    const ST* lb = (const ST*)a.lb;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int n = n0 + wn * TL::WN + i * 16 + 4 * (lane >> 4);
+      float bv[4];
+#pragma unroll
+      for (int v = 0; v < 4; v++) bv[v] = DT_<CT>::to_f32(lb[min(n + v, N - 1)]);
+#pragma unroll
+      for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[i][j][v] = DT_<CT>::round(acc[i][j][v]) + bv[v];
+    }
+  }
 #pragma unroll
   for (int i = 0; i < NI; i++) {
     const int n = n0 + wn * TL::WN + i * 16 + 4 * (lane >> 4);
@@ -551,19 +569,6 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   }
 }
 
-int gemm_device_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-    else
-      cus = 256;
-  }
-  return cus;
-}
-
 template <int CT, int GS, bool SWI, int SZ, int KS>
 hipError_t run_qgemm_sz(const QArgs& a) {
   using TL = GTile<SZ>;
@@ -575,14 +580,13 @@ hipError_t run_qgemm_sz(const QArgs& a) {
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
   k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
+  k.lb = a.lb;
   auto fn = qgemm_kernel<HQ_BITS, CT, GS, SWI, SZ, KS>;
   const size_t lds = (size_t)KS * 2 * (TL::TN + TL::TM) * GLD * 2;
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  static std::atomic<uint64_t> raised{0};
+  {
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), (int)lds, raised);
     if (e != hipSuccess) return e;
-    attr = true;
   }
   const int ont = SWI ? TL::TN / 2 : TL::TN;
   const unsigned ntiles = (unsigned)(((a.N + ont - 1) / ont) * ((a.M + TL::TM - 1) / TL::TM));
@@ -600,7 +604,7 @@ hipError_t run_qgemm_sz(const QArgs& a) {
 // 442.9).
 template <int CT, int GS, bool SWI>
 hipError_t run_qgemm(const QArgs& a) {
-  const int cus = gemm_device_cus();
+  const int cus = device_cu_count();
   auto tiles2 = [&](int64_t tn, int64_t tm) {
     const int64_t ont = SWI ? tn / 2 : tn;
     return ((a.N + ont - 1) / ont) * ((a.M + tm - 1) / tm);
@@ -915,6 +919,7 @@ static void run_qmm_t(const QArgs& a) {
   k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
   k.gshift = __builtin_ctz((unsigned)a.group_size);
+  k.lb = a.lb;
   dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM),
             (unsigned)(a.batch < 65535 ? a.batch : 65535));
   qmm_t_kernel<HQ_BITS, XDT, SDT><<<grid, 256, 0, a.stream>>>(k);

@@ -31,6 +31,7 @@ struct QKern {
   int64_t batch, x_rep, x_batch, w_batch;
   int M, N, K;
   int gshift;
+  const void* lb;  // linear bias [N] or null
 };
 
 static QKern to_kern(const QArgs& a) {
@@ -40,6 +41,7 @@ static QKern to_kern(const QArgs& a) {
   k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
   k.gshift = __builtin_ctz((unsigned)a.group_size);
+  k.lb = a.lb;
   return k;
 }
 
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(256) void qmv_t_kernel(QKern a) {
 #pragma unroll
       for (int m = 0; m < MB; m++) {
         const float v = wave_sum(acc[r][m]);
-        if (lane == 0 && n0 + r < N && m < M) yi[(int64_t)m * N + n0 + r] = DT_<ODT>::from_f32(v);
+        if (lane == 0 && n0 + r < N && m < M) yi[(int64_t)m * N + n0 + r] = linear_out<ODT>(v, a.lb, n0 + r);
       }
   }
 }

@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "hq_common.hpp"
+#include "hq_device.hpp"
 #include "hq_kernels.hpp"
 
 #ifndef HQ_BITS
@@ -53,6 +54,7 @@ struct QXKern {
   int M, N, K;
   int KC;       // K elements staged per chunk (multiple of 128)
   int S;        // segments per wave per chunk
+  const void* lb;  // linear bias [N] or null (batch == 1 only)
 };
 
 template <int XDT> struct XMma;
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(1024) void qmvx_kernel(QXKern a) {
       for (int w2 = 0; w2 < W; w2++)
 #pragma unroll
         for (int h = 0; h < Z; h++) r += red[((w2 * Z + h) * M + m) * 16 + n];
-      if (n0 + n < N) yb[(int64_t)m * N + n0 + n] = DT_<ODT>::from_f32(r);
+      if (n0 + n < N) yb[(int64_t)m * N + n0 + n] = linear_out<ODT>(r, a.lb, n0 + n);
     }
     __syncthreads();  // red is rewritten by the next batch element
   }
@@ -340,6 +342,7 @@ struct PKern {
   // compiler keeps them in registers and emits one v_and_or_b32 per pair (gfx9
   // VOP3 cannot encode 32-bit literals).
   uint32_t nib_mask, off_pair;
+  const void* lb;  // linear bias [N] or null (not with SwiGLU)
 };
 
 // NG consecutive scale values as floats (vector load).
@@ -601,7 +604,7 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
         }
         sum = swiglu_f32(DT_<ODT>::round(gsum[e]), DT_<ODT>::round(sum));
       }
-      if (t * 16 + n < N) ((OS*)a.y)[(int64_t)m * N + t * 16 + n] = DT_<ODT>::from_f32(sum);
+      if (t * 16 + n < N) ((OS*)a.y)[(int64_t)m * N + t * 16 + n] = linear_out<ODT>(sum, a.lb, t * 16 + n);
     }
   };
 
@@ -713,6 +716,7 @@ struct SKern {
   int M, N, K;
   int ntiles;   // ceil(N / 16)
   uint32_t nib_mask, off_pair;
+  const void* lb;  // linear bias [N] or null (not with SwiGLU)
 };
 
 template <int BITS, int XDT, int GS, int MB, int TPB, int RW, bool SWI, bool SPLIT, int S, bool XF>
@@ -971,23 +975,13 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
       }
       float o = hs[0];
       if constexpr (SWI) o = swiglu_f32(DT_<XDT>::round(hs[0]), DT_<XDT>::round(hs[1]));
-      if (tid < M * 16 && t * 16 + (tid & 15) < N)
-        ((st_t<XDT>*)a.y)[(int64_t)(tid >> 4) * N + t * 16 + (tid & 15)] = DT_<XDT>::from_f32(o);
+      if (tid < M * 16 && t * 16 + (tid & 15) < N) {
+        const int n = t * 16 + (tid & 15);
+        ((st_t<XDT>*)a.y)[(int64_t)(tid >> 4) * N + n] =
+            SWI ? DT_<XDT>::from_f32(o) : linear_out<XDT>(o, a.lb, n);
+      }
     }
   }
-}
-
-int device_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-    else
-      cus = 256;
-  }
-  return cus;
 }
 
 // Launches the streaming kernel: K / (RW * 1024) waves per block, TPB tiles
@@ -1006,16 +1000,13 @@ hipError_t run_qmvs(const QArgs& a) {
   k.ntiles = (int)((a.N + 15) / 16);
   k.nib_mask = 0x000F000Fu;
   k.off_pair = XMma<XDT>::OFFB;
+  k.lb = a.lb;
   const int grid = (k.ntiles + TPB - 1) / TPB;
   auto fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true, S, XF>;
   if (lds > 64 * 1024) {
-    static bool big = false;
-    if (!big) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return e;
-      big = true;
-    }
+    static std::atomic<uint64_t> raised{0};
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), 160 * 1024, raised);
+    if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, a.stream, k);
   return hipGetLastError();
@@ -1036,21 +1027,24 @@ inline int qmvp_grid(int ntiles, size_t lds, int vgprs, int W) {
   if (per_cu > 4) per_cu = 4;
   if (per_cu > (4 * waves_per_simd) / W) per_cu = (4 * waves_per_simd) / W;
   if (per_cu < 1) per_cu = 1;
-  const int maxb = per_cu * device_cus();
+  const int maxb = per_cu * device_cu_count();
   const int per = (ntiles + maxb - 1) / maxb;
   return (ntiles + per - 1) / per;
 }
 
 template <int XDT, int SDT, int MB, int GS, int S, bool DX, bool SWI>
 int qmvp_vgprs() {
-  static int vg = 0;
-  if (vg == 0) {
+  // a property of the code object (the same on every gfx950 device)
+  static std::atomic<int> vg{0};
+  int v = vg.load(std::memory_order_relaxed);
+  if (v == 0) {
     hipFuncAttributes fa;
     auto fn = qmvp_kernel<HQ_BITS, XDT, SDT, MB, GS, S, DX, SWI>;
-    vg = (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)) == hipSuccess && fa.numRegs > 0)
-             ? fa.numRegs : 128;
+    v = (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(fn)) == hipSuccess && fa.numRegs > 0)
+            ? fa.numRegs : 128;
+    vg.store(v, std::memory_order_relaxed);
   }
-  return vg;
+  return v;
 }
 
 // Launches the persistent kernel with W waves per block and R rounds per
@@ -1066,16 +1060,15 @@ hipError_t run_qmvp_s(const QArgs& a, int W, int R) {
   k.nib_mask = 0x000F000Fu;
   k.off_pair = XMma<XDT>::OFFB;
   k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
+  k.lb = a.lb;
   const int ntiles = (int)((a.N + 15) / 16);
   k.ntiles = ntiles;
   auto fn = qmvp_kernel<HQ_BITS, XDT, SDT, MB, GS, S, DX, SWI>;
   const int grid = qmvp_grid(ntiles, lds, qmvp_vgprs<XDT, SDT, MB, GS, S, DX, SWI>(), W);
-  static bool big_lds = false;
-  if (lds > 64 * 1024 && !big_lds) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  static std::atomic<uint64_t> raised{0};
+  if (lds > 64 * 1024) {
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), 160 * 1024, raised);
     if (e != hipSuccess) return e;
-    big_lds = true;
   }
   (void)sizeof(C);
   hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, a.stream, k);
@@ -1135,7 +1128,7 @@ hipError_t run_qmvp(const QArgs& a) {
       return 0;
     };
     const int W8 = pick(8), W4 = pick(4);
-    if ((W8 < 8 && ntiles <= 512 && W4 >= W8) || (ntiles >= 16 * device_cus() && W4 == 8))
+    if ((W8 < 8 && ntiles <= 512 && W4 >= W8) || (ntiles >= 16 * device_cu_count() && W4 == 8))
       return run_qmvp_sd<XDT, SDT, MB, GS, 4, SWI>(a, W4, nseg / (4 * W4));
     if (W8 == 0) return hipErrorNotSupported;
     if (!kDirectOk<MB, GS, 8> && qmvp_lds(a, W8, MB, GS, false, SWI) > 160 * 1024)
@@ -1151,6 +1144,7 @@ hipError_t run_qmvx(const QArgs& a) {
   k.lhs = a.lhs; k.rhs = a.rhs;
   k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
+  k.lb = a.lb;
   constexpr int RPH = MB <= 4 ? 4 : 8;
   constexpr int Z = 128 / GS;
   const int kpad = (int)((a.K + 127) / 128 * 128);
@@ -1168,12 +1162,10 @@ hipError_t run_qmvx(const QArgs& a) {
                      (size_t)W * Z * a.M * 16 * 4;
   dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)(a.batch < 65535 ? a.batch : 65535));
   auto fn = qmvx_kernel<HQ_BITS, XDT, SDT, MB, GS>;
-  static bool big_lds = false;  // opt-in to > 64 KB once per instantiation
-  if (lds > 64 * 1024 && !big_lds) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  static std::atomic<uint64_t> raised{0};  // opt-in to > 64 KB once per device
+  if (lds > 64 * 1024) {
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), 160 * 1024, raised);
     if (e != hipSuccess) return e;
-    big_lds = true;
   }
   hipLaunchKernelGGL(fn, grid, dim3(64 * W), lds, a.stream, k);
   return hipGetLastError();

@@ -3,7 +3,8 @@
 * ``QLinear`` -- crates/higgs-models/src/qwen3_next.rs:232-280 (raw weight /
   scales / biases + group_size / bits; ``forward`` = quantized_matmul with
   transpose=true, quantized_forward at 218-227; ``forward_decode_fast`` is
-  the same kernel here, the decode GEMV is the default path).
+  the same kernel here, the decode GEMV is the default path), plus the
+  optional bias of mlx-rs QuantizedLinear (transformer.rs:148-157, 180-191).
 * ``QEmbedding`` -- qwen3_next.rs:284-333: ``forward`` = take rows then
   dequantize (fused: only the selected rows are read); ``as_linear`` = the
   tied lm_head, quantized_matmul against the embedding table
@@ -11,8 +12,9 @@
 * ``DenseSwiGLU`` -- FfnBlock::dense_hidden_fused (qwen3_next.rs:2539-2585):
   gate and up concatenated once, one fused launch per call.
 * ``SwitchGLU`` -- SwitchMlpWeights (qwen3_next.rs:1660-1809) with stacked
-  [experts, N, P] weights: ``forward_gather_global_sort`` and the
-  score-weighted ``moe`` of qwen3_moe.rs:353-357.
+  [experts, N, P] weights: ``forward_gather`` (unsorted),
+  ``forward_gather_global_sort`` and the score-weighted ``moe`` of
+  qwen3_moe.rs:353-357; each projection keeps its own group size and bits.
 """
 from __future__ import annotations
 
@@ -22,11 +24,26 @@ from . import ops
 
 
 class QLinear:
-    def __init__(self, weight, scales, biases, group_size: int = 64, bits: int = 4):
+    """``bias`` (optional, [out_features]) is the layer's additive bias, as on
+    mlx-rs QuantizedLinear for Qwen2-style q/k/v projections
+    (transformer.rs:180-191); it is added in the kernel's epilogue."""
+
+    def __init__(self, weight, scales, biases, group_size: int = 64, bits: int = 4, bias=None):
         self.weight, self.scales, self.biases = weight, scales, biases
         self.group_size, self.bits = group_size, bits
+        self.bias = bias
+
+    @classmethod
+    def from_float(cls, weight: torch.Tensor, group_size: int = 64, bits: int = 4, bias=None):
+        """Quantize a float [out, in] weight on the GPU (mlx_rs::nn::quantize of
+        an nn::Linear, transformer.rs:954-965)."""
+        wq, s, b = ops.quantize(weight, group_size, bits)
+        return cls(wq, s, b, group_size, bits, bias)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.bias is not None:
+            return ops.quantized_linear(x, self.weight, self.scales, self.biases, self.bias,
+                                        self.group_size, self.bits)
         return ops.quantized_matmul(x, self.weight, self.scales, self.biases, True,
                                     self.group_size, self.bits)
 
@@ -89,15 +106,21 @@ class SwitchGLU:
         self.num_experts = gate.weight.shape[0]
 
     def _t(self, l: QLinear):
-        return (l.weight, l.scales, l.biases)
+        # each projection carries its own quantization settings
+        return (l.weight, l.scales, l.biases, l.group_size, l.bits)
+
+    def forward_gather(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """The unsorted path (qwen3_next.rs:1660-1720): x [B, L, D], indices
+        [B, L, top_k] -> [B, L, top_k, D]."""
+        return ops.forward_gather(x, indices, self._t(self.gate), self._t(self.up),
+                                  self._t(self.down))
 
     def forward_gather_global_sort(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """x [B, L, D], indices [B, L, top_k] -> [B, L, top_k, D]."""
         return ops.forward_gather_global_sort(x, indices, self._t(self.gate), self._t(self.up),
-                                              self._t(self.down), self.gate.group_size,
-                                              self.gate.bits)
+                                              self._t(self.down))
 
     def moe(self, x: torch.Tensor, indices: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
         """sum over top_k of scores * expert outputs: [B, L, D]."""
         return ops.moe_block(x, indices, scores, self._t(self.gate), self._t(self.up),
-                             self._t(self.down), self.gate.group_size, self.gate.bits)
+                             self._t(self.down))

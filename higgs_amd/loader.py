@@ -13,7 +13,10 @@ on-disk MLX layout (docs/mlx_rs_capabilities.md:38-52):
   ``.inner.`` inserted, for mlx-rs' nested MaybeQuantized parameters;
 * ``config.json`` ``quantization`` = {group_size, bits} (transformer.rs:57-62),
   with per-layer overrides keyed by the layer path (qwen3_next.rs:3431-3437
-  reads one for the MoE router gate).
+  reads one for the MoE router gate, under the full tensor-name path);
+* a linear layer's optional additive ``<layer>.bias`` (``.inner.bias`` after
+  the remap, lib.rs:1002-1005), present on Qwen2-style q/k/v projections
+  (qkv_bias, transformer.rs:180-191).
 
 The safetensors container is parsed here directly (8-byte little-endian
 header length, JSON header of {name: {dtype, shape, data_offsets}}, then
@@ -158,6 +161,7 @@ class Checkpoint:
 
     def __init__(self, model_path: str, device, prefix: str = ""):
         self.path = model_path
+        self.prefix = prefix
         self.config = load_config(model_path)
         self.tensors: Dict[str, object] = {}
         for f in collect_safetensors_files(model_path):
@@ -186,8 +190,27 @@ class Checkpoint:
                         self.tensors[base + ".biases"])
         raise CheckpointError(f"no quantized weight for {path}")
 
+    def _bias(self, path: str, out_features: int):
+        """The layer's additive bias (``.bias`` or ``.inner.bias``), or None."""
+        for key in (path + ".bias", path + ".inner.bias"):
+            if key in self.tensors:
+                b = self.tensors[key]
+                if tuple(b.shape) != (out_features,):
+                    raise CheckpointError(f"{key}: shape {tuple(b.shape)} is not "
+                                          f"({out_features},)")
+                return b
+        return None
+
     def _params(self, path: str, w, s):
-        gb = quantization_for(self.config, path)
+        # per-layer overrides are keyed by the full tensor path (the prefix
+        # included); then the bare path; then the top-level defaults
+        gb = None
+        if self.prefix:
+            q = self.config.get("quantization") or self.config.get("quantization_config") or {}
+            if (self.prefix + path) in q:
+                gb = quantization_for(self.config, self.prefix + path)
+        if gb is None:
+            gb = quantization_for(self.config, path)
         if gb is None:
             raise CheckpointError(f"{path}: config.json has no quantization for this layer")
         g, bits = gb
@@ -202,7 +225,7 @@ class Checkpoint:
 
         w, s, b = self._triple(path)
         g, bits = self._params(path, w, s)
-        return QLinear(w, s, b, g, bits)
+        return QLinear(w, s, b, g, bits, bias=self._bias(path, w.shape[-2]))
 
     def embedding(self, path: str):
         from .layers import QEmbedding

@@ -11,6 +11,11 @@ same argument names, meanings and validation messages:
   higgs' ``gather_qmm`` (qwen3_next.rs:509-578).
 * ``dequantize(w, scales, biases, group_size, bits)`` -- mlx-rs
   ``ops::dequantize`` (qwen3_next.rs:314).
+* ``quantize(w, group_size, bits)`` -- mlx-rs ``ops::quantize``
+  (qwen3_next.rs:4305-4307, 12942; ``nn::quantize`` at transformer.rs:954-965).
+* ``quantized_linear(x, w, scales, biases, bias, group_size, bits)`` -- mlx-rs
+  ``QuantizedLinear::forward`` (quantized_matmul, then + bias when the layer
+  has one: the Qwen2 q/k/v projections, transformer.rs:180-191).
 * ``dense_hidden_fused`` -- ``FfnBlock::dense_hidden_fused``
   (qwen3_next.rs:2539-2585): gate/up projection and SwiGLU in one launch.
 * ``forward_gather_global_sort`` / ``moe_block`` -- the MoE experts on the
@@ -162,6 +167,42 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return y
 
 
+def quantized_linear(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                     group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """y = x @ deq(w).T + bias for a 2-D ``w`` [N, P]; ``bias`` [N] or None.
+
+    The product is rounded to the output dtype, then the bias is added and the
+    sum rounded (mlx-rs QuantizedLinear: quantized_matmul, then add), in the
+    kernel's epilogue. The bias must have the product's output dtype.
+    """
+    tag = "quantized_linear"
+    if bias is None:
+        return quantized_matmul(x, w, scales, biases, True, group_size, bits)
+    _check_params(tag, group_size, bits)
+    if x.dim() < 1:
+        raise _err(f"[{tag}] x must have at least one dimension.")
+    w, w_inner, w_outer = _extract_dims(tag, x, w, scales, biases, True, group_size, bits)
+    if w.dim() != 2:
+        raise _err(f"[{tag}] The weight of a linear layer is 2-D (got {_shape(w)}).")
+    out_dtype = result_dtype(x.dtype, scales.dtype)
+    if tuple(bias.shape) != (w_outer,):
+        raise _err(f"[{tag}] The bias must have shape ({w_outer},) (got {_shape(bias)}).")
+    if bias.dtype != out_dtype:
+        raise _err(f"[{tag}] The bias dtype ({_dt_name(bias)}) must be the output dtype "
+                   f"{str(out_dtype).replace('torch.', '')}.", _lib.HQ_ERR_UNSUPPORTED)
+    dev = _check_device(tag, x, w, scales, biases, bias)
+    x = x.contiguous()
+    K = x.shape[-1]
+    M = x.numel() // K if K else 0
+    y = torch.empty((*x.shape[:-1], w_outer), dtype=out_dtype, device=dev)
+    _lib.check(_lib.lib().hq_quantized_linear(
+        _ptr(y), _ptr(x), _ptr(w), _ptr(scales.contiguous()), _ptr(biases.contiguous()),
+        _ptr(bias.contiguous()), M, w_outer, K, group_size, bits, _DT[x.dtype],
+        _DT[scales.dtype], _DT[bias.dtype], _stream(dev)))
+    return y
+
+
 def _prefix_broadcast(x_batch_shape: Sequence[int], out_shape: Sequence[int]) -> bool:
     """True if x's batch dims, right-aligned to out_shape, equal a prefix of out_shape
     followed only by 1s -- then x batch element = flat_out_index // (batch/x_batch)."""
@@ -276,6 +317,39 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
     _lib.check(_lib.lib().hq_dequantize(_ptr(out), _ptr(w), _ptr(scales), _ptr(biases), rows, K,
                                         group_size, bits, _DT[scales.dtype], _stream(dev)))
     return out
+
+
+def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4):
+    """MLX affine quantize of a float matrix w [..., K] on the GPU.
+
+    Returns (wq int32 [..., K*bits/32] (uint32 bit patterns, MLX packing),
+    scales, biases [..., K/group_size] in w's dtype), as mlx-rs
+    ``ops::quantize(w, group_size, bits)``: per group, the min or max of larger
+    magnitude becomes the bias and an exact multiple of the scale, so 0 is
+    representable; every operation rounds to w's dtype.
+    """
+    tag = "quantize"
+    _check_params(tag, group_size, bits)
+    if w.dim() < 2:
+        raise _err(f"[{tag}] The matrix to be quantized must have at least 2 dimension but it "
+                   f"has only {w.dim()}.")
+    if w.dtype not in _DT:
+        raise _err(f"[{tag}] Only real floating types can be quantized (got {_dt_name(w)}).")
+    K = w.shape[-1]
+    if K % group_size:
+        raise _err(f"[{tag}] The last dimension of the matrix needs to be divisible by the "
+                   f"quantization group size {group_size}. However the provided matrix has "
+                   f"shape {_shape(w)}")
+    dev = _check_device(tag, w)
+    w = w.contiguous()
+    rows = w.numel() // K if K else 0
+    wq = torch.empty((*w.shape[:-1], K * bits // 32), dtype=torch.int32, device=dev)
+    scales = torch.empty((*w.shape[:-1], K // group_size), dtype=w.dtype, device=dev)
+    biases = torch.empty_like(scales)
+    if rows:
+        _lib.check(_lib.lib().hq_quantize(_ptr(wq), _ptr(scales), _ptr(biases), _ptr(w), rows, K,
+                                          group_size, bits, _DT[w.dtype], _stream(dev)))
+    return wq, scales, biases
 
 
 def embedding(indices: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
@@ -415,11 +489,23 @@ def gather_qmm_swiglu(x: torch.Tensor, gate: Sequence[torch.Tensor], up: Sequenc
     h = torch.empty((batch, M, N), dtype=result_dtype(x.dtype, sg.dtype), device=dev)
     if h.numel() == 0:
         return h
-    _lib.check(_lib.lib().hq_gather_qmm_swiglu(
+    rc = _lib.lib().hq_gather_qmm_swiglu(
         _ptr(h), _ptr(x), _ptr(wg), _ptr(sg.contiguous()), _ptr(bg.contiguous()), _ptr(wu),
         _ptr(su.contiguous()), _ptr(bu.contiguous()), _ptr(lhs), _ptr(rhs), batch,
         max(x_batch, 1), wg.shape[0], M, N, K, group_size, bits, _DT[x.dtype], _DT[sg.dtype],
-        _stream(dev)))
+        _stream(dev))
+    if rc == _lib.HQ_ERR_UNSUPPORTED:
+        # shapes or dtypes the fused grouped kernel does not take (float32
+        # activations, mixed dtypes, K % 64 != 0): the reference's own form,
+        # two sorted gather_qmm calls and swiglu (qwen3_next.rs:1764-1787)
+        xs = x.reshape(-1, M, K)
+        if lhs is None:  # the null-lhs broadcast, made explicit
+            lhs = (torch.arange(batch, dtype=torch.int64, device=dev) //
+                   (batch // max(x_batch, 1))).to(torch.int32)
+        g = gather_qmm(xs, wg, sg, bg, lhs, rhs, True, group_size, bits, True)
+        u = gather_qmm(xs, wu, su, bu, lhs, rhs, True, group_size, bits, True)
+        return swiglu(g, u)
+    _lib.check(rc)
     return h
 
 
@@ -474,26 +560,49 @@ def moe_combine(y_sorted: torch.Tensor, inv_order: torch.Tensor,
     return out
 
 
+def _proj(t: Sequence, group_size: int, bits: int):
+    """A projection argument: (w, scales, biases) uses the call's group_size
+    and bits; (w, scales, biases, group_size, bits) carries its own, as each
+    SwitchLinear of a mixed-precision checkpoint does."""
+    if len(t) == 5:
+        return tuple(t[:3]), int(t[3]), int(t[4])
+    if len(t) == 3:
+        return tuple(t), group_size, bits
+    raise _err("[switch_glu] a projection is (w, scales, biases[, group_size, bits]).")
+
+
 def _switch_sorted(x, indices, gate, up, down, group_size, bits):
-    """Sort, fused gate/up + SwiGLU, down; returns (y_sorted [n, D], inv_order)."""
-    wg = gate[0]
-    E = wg.shape[0]
+    """Sort, gate/up + SwiGLU, down; returns (y_sorted [n, D], inv_order).
+
+    Each projection uses its own (group_size, bits) (qwen3_next.rs:1764-1800
+    passes gate_proj's, up_proj's and down_proj's settings to their own
+    gather_qmm). Gate and up run as one fused launch when they share their
+    settings; otherwise as two sorted gather_qmm calls and swiglu."""
+    (g_t, g_gs, g_b) = _proj(gate, group_size, bits)
+    (u_t, u_gs, u_b) = _proj(up, group_size, bits)
+    (d_t, d_gs, d_b) = _proj(down, group_size, bits)
+    E = g_t[0].shape[0]
     D = x.shape[-1]
     order, inv, srt, tok = moe_sort(indices, E)
     xf = x.reshape(-1, 1, D)
-    h = gather_qmm_swiglu(xf, gate, up, tok, srt, group_size, bits)        # [n, 1, I]
-    y = gather_qmm(h, down[0], down[1], down[2], None, srt, True, group_size, bits, True)
+    if (g_gs, g_b) == (u_gs, u_b):
+        h = gather_qmm_swiglu(xf, g_t, u_t, tok, srt, g_gs, g_b)        # [n, 1, I]
+    else:
+        gt = gather_qmm(xf, *g_t, tok, srt, True, g_gs, g_b, True)
+        ut = gather_qmm(xf, *u_t, tok, srt, True, u_gs, u_b, True)
+        h = swiglu(gt, ut)
+    y = gather_qmm(h, *d_t, None, srt, True, d_gs, d_b, True)
     return y.reshape(-1, y.shape[-1]), inv
 
 
 def forward_gather_global_sort(x: torch.Tensor, indices: torch.Tensor,
-                               gate: Sequence[torch.Tensor], up: Sequence[torch.Tensor],
-                               down: Sequence[torch.Tensor], group_size: int = 64,
-                               bits: int = 4) -> torch.Tensor:
+                               gate: Sequence, up: Sequence, down: Sequence,
+                               group_size: int = 64, bits: int = 4) -> torch.Tensor:
     """SwitchMlpWeights::forward_gather_global_sort (qwen3_next.rs:1731-1809).
 
     x: [B, L, D]; indices: [B, L, top_k]; gate/up/down: (w, scales, biases)
-    of SwitchLinear weights [E, N, P]. Returns [B, L, top_k, D] in the
+    of SwitchLinear weights [E, N, P], optionally followed by that
+    projection's own group_size and bits. Returns [B, L, top_k, D] in the
     original (unsorted) order. The x gather rides on gather_qmm's
     lhs_indices, gate/up/SwiGLU is one launch, and the unsort is a combine
     with unit scores (an exact row copy).
@@ -506,14 +615,40 @@ def forward_gather_global_sort(x: torch.Tensor, indices: torch.Tensor,
     return out.reshape(B, L, top_k, -1)
 
 
+def forward_gather(x: torch.Tensor, indices: torch.Tensor, gate: Sequence, up: Sequence,
+                   down: Sequence, group_size: int = 64, bits: int = 4) -> torch.Tensor:
+    """SwitchMlpWeights::forward_gather, the unsorted path (qwen3_next.rs:1660-1720).
+
+    x: [B, L, D] is viewed as [B, L, 1, 1, D] and broadcast against indices
+    [B, L, top_k]: gate and up are gather_qmm calls with the null-lhs
+    broadcast, then swiglu, then down with the same indices; the result
+    [B, L, top_k, 1, D] is squeezed to [B, L, top_k, D]. Every (token, slot)
+    row reads its expert's weights on its own (no sort), which is why the
+    reference moved to the global-sort path; both must agree
+    (qwen3_next.rs:4431-4530).
+    """
+    (g_t, g_gs, g_b) = _proj(gate, group_size, bits)
+    (u_t, u_gs, u_b) = _proj(up, group_size, bits)
+    (d_t, d_gs, d_b) = _proj(down, group_size, bits)
+    B, L, D = x.shape
+    top_k = indices.shape[-1]
+    xe = x.reshape(B, L, 1, 1, D)
+    g = gather_qmm(xe, *g_t, None, indices, True, g_gs, g_b, False)      # [B, L, k, 1, I]
+    u = gather_qmm(xe, *u_t, None, indices, True, u_gs, u_b, False)
+    h = swiglu(g, u)
+    y = gather_qmm(h, *d_t, None, indices, True, d_gs, d_b, False)      # [B, L, k, 1, D]
+    return y.reshape(B, L, top_k, -1)
+
+
 def moe_block(x: torch.Tensor, indices: torch.Tensor, scores: torch.Tensor,
-              gate: Sequence[torch.Tensor], up: Sequence[torch.Tensor],
-              down: Sequence[torch.Tensor], group_size: int = 64, bits: int = 4) -> torch.Tensor:
+              gate: Sequence, up: Sequence, down: Sequence, group_size: int = 64,
+              bits: int = 4) -> torch.Tensor:
     """Experts of the MoE block after routing (qwen3_moe.rs:353-357):
     forward_gather_global_sort(x, indices) * scores, summed over top_k.
 
     x: [B, L, D]; indices, scores: [B, L, top_k]. Returns [B, L, D]. Four
-    launches: sort, gate/up + SwiGLU, down, unsort + weighted sum.
+    launches (sort, gate/up + SwiGLU, down, unsort + weighted sum) when gate
+    and up share their quantization settings.
     """
     y, inv = _switch_sorted(x, indices, gate, up, down, group_size, bits)
     return moe_combine(y, inv, scores)

@@ -20,8 +20,11 @@
  *    hq_result_dtype(x_dtype, s_dtype) (equal -> same, mixed -> float32).
  *  - Return value: HQ_OK (0) or an hq_status error; the message of the last
  *    error on the calling thread is returned by hq_last_error().
- *  - Calls on one stream are ordered; the library keeps no per-call state,
- *    so concurrent calls from several threads on different streams are safe.
+ *  - Calls on one stream are ordered. The library keeps no per-call state;
+ *    its only shared state is one-time launcher setup per device (the CU
+ *    count, opting kernels into more than 64 KB of LDS), held in atomics, so
+ *    concurrent calls from several threads on different streams or devices
+ *    are safe.
  */
 #ifndef HIGGS_QMM_H
 #define HIGGS_QMM_H
@@ -32,7 +35,7 @@
 extern "C" {
 #endif
 
-#define HQ_ABI_VERSION 2
+#define HQ_ABI_VERSION 3
 
 typedef enum hq_status {
   HQ_OK = 0,
@@ -79,6 +82,31 @@ int hq_quantized_matmul(void* y, const void* x, const uint32_t* w,
                         const void* scales, const void* biases, int64_t M,
                         int64_t N, int64_t K, int transpose, int group_size,
                         int bits, int x_dtype, int s_dtype, void* stream);
+
+/*
+ * Quantized linear layer with an optional bias:  y = x . deq(W)^T + bias.
+ *
+ * Replaces mlx-rs QuantizedLinear::forward (quantized_matmul with
+ * transpose=true, then add the bias when the layer has one), which
+ * mlx_rs::nn::quantize makes of every MaybeQuantized nn::Linear at load
+ * (crates/higgs-models/src/transformer.rs:954-965). Qwen2-style checkpoints
+ * give q_proj, k_proj and v_proj a bias (qkv_bias, transformer.rs:180-191),
+ * stored as <layer>.bias / .inner.bias (crates/higgs-models/src/lib.rs:
+ * 1002-1005).
+ *
+ *   x: [M, K]; w: [N, K*bits/32]; scales/biases: [N, K/group_size];
+ *   bias: [N] of bias_dtype, or NULL (then this is hq_quantized_matmul with
+ *   transpose = 1); y: [M, N] of hq_result_dtype(x_dtype, s_dtype).
+ *
+ * Rounding: y = round(round(x . deq(W)^T) + bias) -- the product is rounded
+ * to the output dtype as MLX materialises it, then the sum is rounded (one
+ * rounding in all for float32 output). bias_dtype must equal the output
+ * dtype (HQ_ERR_UNSUPPORTED otherwise; MLX would promote the sum).
+ */
+int hq_quantized_linear(void* y, const void* x, const uint32_t* w,
+                        const void* scales, const void* biases, const void* bias,
+                        int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                        int x_dtype, int s_dtype, int bias_dtype, void* stream);
 
 /*
  * Batched quantized matmul with expert gather.
@@ -137,6 +165,34 @@ int hq_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales,
 int hq_dequantize(void* out, const uint32_t* w, const void* scales,
                   const void* biases, int64_t rows, int64_t K, int group_size,
                   int bits, int s_dtype, void* stream);
+
+/*
+ * Affine group quantization: the inverse direction of hq_dequantize.
+ *
+ * Replaces mlx-rs ops::quantize(w, group_size, bits) -- used by higgs' tests
+ * to make quantized operands (crates/higgs-models/src/qwen3_next.rs:
+ * 4305-4307, 12942) and by mlx_rs::nn::quantize, which quantizes every
+ * MaybeQuantized layer of a float checkpoint at load (crates/higgs-models/
+ * src/transformer.rs:954-965).
+ *
+ *   w: [rows, K] of dtype; wq: uint32 [rows, K*bits/32] (MLX packing);
+ *   scales, biases: [rows, K/group_size] of dtype. K % group_size == 0,
+ *   rows * K < 2^40.
+ *
+ * Per group of group_size consecutive elements, every operation computed in
+ * float32 and rounded to dtype (MLX's op-by-op form):
+ *   mx = max, mn = min, n_bins = 2^bits - 1,
+ *   scale = max((mx - mn) / n_bins, dtype(1e-7));
+ *   if |mn| > |mx| the edge is mn, else the edge is mx and scale = -scale;
+ *   q0 = rint(edge / scale); if q0 != 0: scale = edge / q0, bias = edge,
+ *   else bias = 0;  q = clip(rint((w - bias) / scale), 0, n_bins).
+ * The edge of larger magnitude is an exact multiple of the scale, so w = 0
+ * maps to an integer code (zero is representable). rint rounds half to even;
+ * divisions are IEEE. NaN inputs give unspecified codes.
+ */
+int hq_quantize(uint32_t* wq, void* scales, void* biases, const void* w,
+                int64_t rows, int64_t K, int group_size, int bits, int dtype,
+                void* stream);
 
 /*
  * Row gather then dequantize: out[i] = deq(W[indices[i]]), i in [0, n).

@@ -66,6 +66,7 @@ def lib():
         L.hqo_gather_sort.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp]
         L.hqo_swiglu.argtypes = [_vp, _vp, _int, _i64, _vp]
         L.hqo_moe_combine.argtypes = [_vp, _int, _vp, _vp, _int, _i64, _i64, _i64, _vp]
+        L.hqo_quantize.argtypes = [_vp, _int, _i64, _i64, _int, _int, _vp, _vp, _vp]
         L.hqo_num_threads.restype = _int
         _lib = L
     return _lib
@@ -244,6 +245,23 @@ def moe_combine(y: np.ndarray, dtype: int, inv: np.ndarray, scores: np.ndarray,
     out = np.empty((tokens, D), y.dtype)
     lib().hqo_moe_combine(_p(y), dtype, _p(inv), _p(scores), sdtype, tokens, top_k, D, _p(out))
     return out
+
+
+def quantize(w: np.ndarray, dtype: int, group_size: int, bits: int):
+    """MLX affine quantize of w [..., K] (float32 values, or uint16 bit patterns
+    of a 16-bit dtype). Returns (wq u32 [..., K*bits/32], scales, biases
+    [..., K/group_size] in dtype)."""
+    w = np.ascontiguousarray(w)
+    K = w.shape[-1]
+    rows = w.size // K if K else 0
+    G = K // group_size
+    wq = np.empty(w.shape[:-1] + (K * bits // 32,), np.uint32)
+    sdt = np.float32 if dtype == F32 else np.uint16
+    s = np.empty(w.shape[:-1] + (G,), sdt)
+    b = np.empty(w.shape[:-1] + (G,), sdt)
+    _check(lib().hqo_quantize(_p(w), dtype, rows, K, group_size, bits, _p(wq), _p(s), _p(b)),
+           "quantize")
+    return wq, s, b
 
 
 def num_threads() -> int:

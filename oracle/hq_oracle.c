@@ -441,3 +441,78 @@ void hqo_moe_combine(const void* y, int dtype, const uint32_t* inv, const void* 
   }
 }
 
+
+/* ------------------------------------------------------------------------ */
+/* quantize                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * MLX affine quantize, op by op in the weights' dtype T (mlx-rs
+ * ops::quantize(w, group_size, bits), called by higgs' tests at
+ * crates/higgs-models/src/qwen3_next.rs:4305-4307 and 12942, and by
+ * mlx_rs::nn::quantize for float checkpoints, transformer.rs:954-965).
+ * The algorithm is MLX's, which is not in /root/reference (PARITY UNPINNED
+ * against MLX itself; pinned here by what the mathematics fixes, see
+ * tests/test_oracle.py). Per group of group_size consecutive elements, each
+ * operation computed in float and rounded to T:
+ *   mx = max(w), mn = min(w), n_bins = 2^bits - 1
+ *   scale = max((mx - mn) / n_bins, T(1e-7))
+ *   if |mn| > |mx|: edge = mn            else: edge = mx, scale = -scale
+ *   q0 = rint(edge / scale)
+ *   if q0 != 0: scale = edge / q0, bias = edge    else: bias = 0
+ *   q = clip(rint((w - bias) / scale), 0, n_bins)   (NaN -> 0)
+ * so that w = 0 dequantizes to exactly 0. q is packed LSB-first (hqo_pack).
+ */
+static float quant_group(const void* w, int dtype, int64_t base, int gs, int bits, uint32_t* q,
+                         float* bias_out) {
+  const float n_bins = (float)((1 << bits) - 1);
+  const float eps = round_dt(1e-7f, dtype);
+  float mx = load_dt(w, dtype, base), mn = mx;
+  for (int i = 1; i < gs; i++) {
+    const float v = load_dt(w, dtype, base + i);
+    if (v > mx) mx = v;
+    if (v < mn) mn = v;
+  }
+  float scale = round_dt(round_dt(mx - mn, dtype) / n_bins, dtype);
+  if (!(scale > eps)) scale = eps;
+  const int side = fabsf(mn) > fabsf(mx);
+  if (!side) scale = -scale;
+  const float edge = side ? mn : mx;
+  const float q0 = rintf(round_dt(edge / scale, dtype));
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = round_dt(edge / q0, dtype);
+    bias = edge;
+  }
+  for (int i = 0; i < gs; i++) {
+    const float v = load_dt(w, dtype, base + i);
+    float t = rintf(round_dt(round_dt(v - bias, dtype) / scale, dtype));
+    if (!(t >= 0.0f)) t = 0.0f;
+    if (t > n_bins) t = n_bins;
+    q[i] = (uint32_t)t;
+  }
+  *bias_out = bias;
+  return scale;
+}
+
+int hqo_quantize(const void* w, int dtype, int64_t rows, int64_t K, int group_size, int bits,
+                 uint32_t* wq, void* scales, void* biases) {
+  if (!(bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8)) return -1;
+  if (!(group_size == 32 || group_size == 64 || group_size == 128)) return -1;
+  if (rows < 0 || K <= 0 || K % group_size) return -1;
+  const int64_t G = K / group_size;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++) {
+    uint32_t* q = (uint32_t*)malloc((size_t)K * sizeof(uint32_t));
+    for (int64_t g = 0; g < G; g++) {
+      float b;
+      const float s = quant_group(w, dtype, r * K + g * group_size, group_size, bits,
+                                  q + g * group_size, &b);
+      store_dt(scales, dtype, r * G + g, s);
+      store_dt(biases, dtype, r * G + g, b);
+    }
+    hqo_pack(q, 1, K, bits, wq + r * (K * bits / 32));
+    free(q);
+  }
+  return 0;
+}

@@ -23,6 +23,9 @@
  *                   y = x . deq(W) for transpose=0.
  *   - gather_qmm:   y[i] = x[lhs[i]] . deq(W[rhs[i]])^T
  *                   (qwen3_next.rs:509-578; lhs null sentinel = broadcast).
+ *   - quantize:     MLX's affine quantize (ops::quantize, used at
+ *                   qwen3_next.rs:4305-4307, 12942; nn::quantize at
+ *                   transformer.rs:954-965), op by op in the weights' dtype.
  *   - gather sort:  order = stable argsort(idx), inv = argsort(order),
  *                   token = order / top_k (qwen3_next.rs:1748-1761,
  *                   benchmarks/bench_moe_sort.py:77-84).
@@ -112,6 +115,15 @@ void hqo_swiglu(const void* gate, const void* up, int dtype, int64_t n, void* ou
  * out: [tokens, D] of dtype. */
 void hqo_moe_combine(const void* y, int dtype, const uint32_t* inv, const void* scores,
                      int sdtype, int64_t tokens, int64_t top_k, int64_t D, void* out);
+
+/* MLX affine quantize, op by op in dtype (each operation's result rounded to
+ * dtype): w [rows, K] of dtype -> wq u32 [rows, K*bits/32] (LSB-first),
+ * scales/biases [rows, K/group_size] of dtype. Per group: the min/max edge of
+ * larger magnitude becomes the bias and an exact multiple of the scale, so 0
+ * is representable (see hq_oracle.c). NaN inputs are outside the contract.
+ * Returns 0, or -1 on bad arguments. */
+int hqo_quantize(const void* w, int dtype, int64_t rows, int64_t K, int group_size, int bits,
+                 uint32_t* wq, void* scales, void* biases);
 
 int hqo_num_threads(void);
 

@@ -21,19 +21,28 @@ LAYERS = {
 }
 
 
-def write_checkpoint(path: str, seed: int = 5, sharded: bool = True, inner: bool = False):
-    """Returns {layer: (w, s, b, bits, group_size)} of what was written."""
+def write_checkpoint(path: str, seed: int = 5, sharded: bool = True, inner: bool = False,
+                     prefix: str = "", bias_layers=()):
+    """Returns {layer: (w, s, b, bits, group_size)} of what was written; with
+    ``bias_layers`` also {layer + ".bias": bf16 bits [rows]} (a Qwen2-style
+    additive linear bias, stored as ``<layer>.bias``). ``prefix`` is put in
+    front of every tensor name and of the per-layer override key, as
+    multimodal checkpoints nest the language model."""
     os.makedirs(path, exist_ok=True)
     written, tensors = {}, {}
     for i, (name, (rows, cols, bits, g)) in enumerate(LAYERS.items()):
         w, s, b = gen.np_quantized(seed + i, rows, cols, bits, g)
-        key = name + (".inner" if inner else "")
+        key = prefix + name + (".inner" if inner else "")
+        if name in bias_layers:
+            lb = gen.np_x_bf16(seed + 100 + i, (rows,))
+            tensors[key + ".bias"] = torch.from_numpy(lb.view(np.int16)).view(torch.bfloat16)
+            written[name + ".bias"] = lb
         tensors[key + ".weight"] = torch.from_numpy(w.astype(np.uint32)).view(torch.uint32)
         # scales / biases as bfloat16 (MLX stores them as float16 or bfloat16)
         tensors[key + ".scales"] = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16)
         tensors[key + ".biases"] = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
         written[name] = (w, s, b, bits, g)
-    tensors["model.norm.weight"] = torch.ones(256, dtype=torch.float32)
+    tensors[prefix + "model.norm.weight"] = torch.ones(256, dtype=torch.float32)
     names = sorted(tensors)
     shards = [names[: len(names) // 2], names[len(names) // 2:]] if sharded else [names]
     weight_map = {}
@@ -49,7 +58,7 @@ def write_checkpoint(path: str, seed: int = 5, sharded: bool = True, inner: bool
             json.dump({"metadata": {}, "weight_map": weight_map}, f)
     cfg = {"model_type": "llama",
            "quantization": {"group_size": 64, "bits": 4,
-                            "model.layers.0.mlp.gate": {"group_size": 64, "bits": 8}}}
+                            prefix + "model.layers.0.mlp.gate": {"group_size": 64, "bits": 8}}}
     with open(os.path.join(path, "config.json"), "w") as f:
         json.dump(cfg, f)
     return written

@@ -231,3 +231,86 @@ def test_moe_sort_and_combine_reject():
     assert "NULL" in _lib.last_error()
     assert L.hq_moe_combine(FAKE + 2, FAKE, FAKE, FAKE, 4, 8, 2048, 2, 2, None) == 1
     assert "aligned" in _lib.last_error()
+
+
+# --- quantized_linear (bias epilogue) and quantize: validation before launch --
+
+def qlin(**kw):
+    a = dict(y=FAKE, x=FAKE, w=FAKE, s=FAKE, b=FAKE, lb=FAKE, M=1, N=64, K=128, g=64, bits=4,
+             xdt=2, sdt=2, bdt=2)
+    a.update(kw)
+    return _lib.lib().hq_quantized_linear(a["y"], a["x"], a["w"], a["s"], a["b"], a["lb"],
+                                          a["M"], a["N"], a["K"], a["g"], a["bits"], a["xdt"],
+                                          a["sdt"], a["bdt"], None)
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(bits=7), 1, "bits 7 is not supported"),
+    (dict(K=96), 1, "divisible by the group size"),
+    (dict(bdt=9), 1, "the bias has dtype code 9"),
+    (dict(bdt=0), 2, "must be the output dtype"),            # bf16 product, f32 bias
+    (dict(xdt=2, sdt=1, bdt=2), 2, "must be the output dtype"),  # mixed -> f32 output
+    (dict(y=0), 1, "NULL"),
+    (dict(x=FAKE + 2), 1, "16-byte aligned"),
+])
+def test_quantized_linear_rejects(kw, code, needle):
+    assert qlin(**kw) == code
+    assert needle in _lib.last_error()
+
+
+def test_quantized_linear_without_bias_ignores_its_dtype():
+    # a NULL bias is plain quantized_matmul: the bias dtype code is not read
+    assert qlin(lb=None, bdt=9, M=0) == 0
+    assert qlin(lb=None, bdt=9, bits=7) == 1 and "bits 7" in _lib.last_error()
+
+
+def quant(**kw):
+    a = dict(wq=FAKE, s=FAKE, b=FAKE, w=FAKE, rows=4, K=128, g=64, bits=4, dt=2)
+    a.update(kw)
+    return _lib.lib().hq_quantize(a["wq"], a["s"], a["b"], a["w"], a["rows"], a["K"], a["g"],
+                                  a["bits"], a["dt"], None)
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(bits=1), "bits 1 is not supported"),
+    (dict(g=48), "group size 48 is not supported"),
+    (dict(K=96), "divisible by the group size"),
+    (dict(K=0), "divisible by the group size"),
+    (dict(rows=-1), "divisible by the group size"),
+    (dict(dt=5), "floating"),
+    (dict(wq=0), "NULL"),
+    (dict(w=FAKE + 8), "16-byte aligned"),
+    (dict(wq=FAKE + 2), "4-byte aligned"),
+    (dict(dt=0, s=FAKE + 2), "float32 scales and biases must be 4-byte aligned"),
+])
+def test_quantize_rejects(kw, needle):
+    assert quant(**kw) == _lib.HQ_ERR_INVALID_ARGUMENT
+    assert needle in _lib.last_error()
+
+
+def test_quantize_empty_succeeds_without_gpu():
+    assert quant(rows=0) == 0
+
+
+def test_facade_quantize_and_linear_errors():
+    w, s, b = _q()
+    x = torch.zeros(1, 128, dtype=torch.bfloat16)
+    with pytest.raises(HiggsQmmError, match="must have shape"):
+        ops.quantized_linear(x, w, s, b, torch.zeros(3, dtype=torch.bfloat16))
+    with pytest.raises(HiggsQmmError, match="must be the output dtype"):
+        ops.quantized_linear(x, w, s, b, torch.zeros(64, dtype=torch.float32))
+    with pytest.raises(HiggsQmmError, match="divisible by the quantization group size"):
+        ops.quantize(torch.zeros(4, 96), 64, 4)
+    with pytest.raises(HiggsQmmError, match="Only real floating types can be quantized"):
+        ops.quantize(torch.zeros(4, 128, dtype=torch.int32), 64, 4)
+    with pytest.raises(HiggsQmmError, match="must live on the GPU"):
+        ops.quantize(torch.zeros(4, 128), 64, 4)
+
+
+def test_switch_projection_settings():
+    """Each SwitchLinear projection may carry its own (group_size, bits)."""
+    t3 = (1, 2, 3)
+    assert ops._proj(t3, 64, 4) == ((1, 2, 3), 64, 4)
+    assert ops._proj((1, 2, 3, 32, 8), 64, 4) == ((1, 2, 3), 32, 8)
+    with pytest.raises(HiggsQmmError):
+        ops._proj((1, 2), 64, 4)

@@ -93,3 +93,19 @@ def test_switch_glu_moe_matches_block(dev):
     per = sw.forward_gather_global_sort(x, idx)                    # [1, T, k, D]
     ref = (per.float() * sc.float()[..., None]).sum(-2)
     assert (out.float() - ref).abs().max().item() <= 1e-2 * ref.abs().max().item()
+
+
+@pytest.mark.parametrize("M", [1, 200])
+def test_linear_with_bias_from_checkpoint(tmp_path, dev, M):
+    """A Qwen2-style q_proj with its bias (transformer.rs:180-191) loaded from
+    an MLX checkpoint, forward against the oracle."""
+    d = str(tmp_path)
+    q = "model.layers.0.self_attn.q_proj"
+    written = write_checkpoint(d, seed=31, bias_layers=(q,))
+    lin = loader.Checkpoint(d, dev).linear(q)
+    w, s, b, bits, g = written[q]
+    x = gen.np_x_bf16(60 + M, (M, 256))
+    y = lin(torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(dev))
+    ref = O.qmm_f64(x, O.BF16, w, s, b, O.BF16, g, bits) + \
+        gen.bf16_bits_to_f32(written[q + ".bias"]).astype(np.float64)[None, :]
+    assert rel_err(to_host_f64(y), ref) <= 1e-2

@@ -120,3 +120,98 @@ def test_sorted_gather_small_matches_per_expert(dev, M):
     for i, e in enumerate(rhs):
         one = ops.quantized_matmul(x[i], W[e], S[e], B[e], True, G, BITS)
         assert (y[i].float() - one.float()).abs().max().item() <= 1e-2 * one.float().abs().max().item()
+
+
+def _block_oracle(x_bits, idx, scs, projs, tokens_to_check):
+    """fp64 expert block for a few tokens with per-projection (group, bits):
+    gate/up rounded to bf16, swiglu, down rounded, then the oracle combine."""
+    (gw, gs, gb, gg, gbits), (uw, us, ub, ug, ubits), (dw, ds, db, dg, dbits) = projs
+    out = {}
+    k = idx.shape[1]
+    for t in tokens_to_check:
+        ys = []
+        for j in range(k):
+            e = int(idx[t, j])
+            g = O.from_f32(O.qmm_f64(x_bits[t:t + 1], O.BF16, gw[e], gs[e], gb[e], O.BF16, gg,
+                                     gbits).astype(np.float32), O.BF16)
+            u = O.from_f32(O.qmm_f64(x_bits[t:t + 1], O.BF16, uw[e], us[e], ub[e], O.BF16, ug,
+                                     ubits).astype(np.float32), O.BF16)
+            h = O.swiglu(g, u, O.BF16)
+            ys.append(O.from_f32(O.qmm_f64(h, O.BF16, dw[e], ds[e], db[e], O.BF16, dg, dbits)
+                                 .astype(np.float32), O.BF16)[0])
+        ref = O.moe_combine(np.stack(ys), O.BF16, np.arange(k, dtype=np.uint32), scs[t:t + 1],
+                            O.BF16)
+        out[t] = O.to_f32(ref, O.BF16)[0].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("down_bits,down_g", [(8, 64), (4, 32)])
+def test_moe_block_mixed_projection_widths(dev, down_bits, down_g):
+    """A mixed-precision checkpoint quantizes switch_mlp.down_proj with other
+    settings than gate/up; each gather_qmm uses its own projection's
+    (qwen3_next.rs:1764-1800). SwitchGLU carries them per projection."""
+    from higgs_amd import layers
+
+    tokens, k, Ex, D, I = 64, 4, 16, 512, 256
+    gate = gen.torch_quantized(90, I, D, 4, 64, dev, lead=(Ex,))
+    up = gen.torch_quantized(91, I, D, 4, 64, dev, lead=(Ex,))
+    down = gen.torch_quantized(92, D, I, down_bits, down_g, dev, lead=(Ex,))
+    sw = layers.SwitchGLU(layers.QLinear(*gate, 64, 4), layers.QLinear(*up, 64, 4),
+                          layers.QLinear(*down, down_g, down_bits))
+    idx = gen.topk_routing(93, tokens, Ex, k)
+    x = gen.torch_x(94, (1, tokens, D), dev)
+    sc = torch.softmax(gen.torch_x(95, (1, tokens, k), dev).float(), -1).to(torch.bfloat16)
+    out = sw.moe(x, idx_dev(idx, dev).reshape(1, tokens, k), sc)
+    host = lambda t: (t[0].cpu().numpy().view(np.uint32), _host(t[1]), _host(t[2]))
+    projs = (host(gate) + (64, 4), host(up) + (64, 4), host(down) + (down_g, down_bits))
+    ref = _block_oracle(_host(x).reshape(tokens, D), idx, _host(sc).reshape(tokens, k), projs,
+                        (0, 9, 33, 63))
+    got = out.float().cpu().numpy().reshape(tokens, D).astype(np.float64)
+    for t, r in ref.items():
+        assert rel_err(got[t], r) <= 1e-2, t
+    # mixed gate/up settings take the unfused gate/up path: same result
+    sw2 = layers.SwitchGLU(layers.QLinear(*gate, 64, 4), layers.QLinear(*up, 64, 4),
+                           layers.QLinear(*down, down_g, down_bits))
+    y_sorted = sw2.forward_gather_global_sort(x.reshape(1, tokens, D),
+                                              idx_dev(idx, dev).reshape(1, tokens, k))
+    assert tuple(y_sorted.shape) == (1, tokens, k, D)
+
+
+def test_switch_forward_gather_equals_global_sort(dev):
+    """SwitchGLU.forward_gather (the unsorted path, qwen3_next.rs:1660-1720)
+    equals forward_gather_global_sort (qwen3_next.rs:4431-4530 asserts it)."""
+    from higgs_amd import layers
+
+    B, L, k, Ex, D, I = 2, 24, 4, 8, 256, 192
+    qs = [gen.torch_quantized(96 + j, *nk, 4, 64, dev, lead=(Ex,))
+          for j, nk in enumerate(((I, D), (I, D), (D, I)))]
+    sw = layers.SwitchGLU(*(layers.QLinear(*t, 64, 4) for t in qs))
+    idx = idx_dev(gen.topk_routing(99, B * L, Ex, k).reshape(B, L, k), dev)
+    x = gen.torch_x(100, (B, L, D), dev)
+    a = sw.forward_gather(x, idx).float()
+    b = sw.forward_gather_global_sort(x, idx).float()
+    assert a.shape == b.shape == (B, L, k, D)
+    assert (a - b).abs().max().item() <= 1e-2 * b.abs().max().item()
+
+
+def test_gather_qmm_swiglu_float32_activations_fall_back(dev):
+    """fp32 activations are outside the fused grouped kernel: the facade runs
+    the reference's own form (two sorted gather_qmm calls and swiglu)."""
+    tokens, k, Ex, D, I = 32, 2, 4, 256, 128
+    gate = gen.torch_quantized(101, I, D, 4, 64, dev, lead=(Ex,), dtype=torch.float32)
+    up = gen.torch_quantized(102, I, D, 4, 64, dev, lead=(Ex,), dtype=torch.float32)
+    idx = gen.topk_routing(103, tokens, Ex, k)
+    order, inv, srt, tok = O.gather_sort(idx, k)
+    x = gen.torch_x(104, (tokens, 1, D), dev, dtype=torch.float32)
+    h = ops.gather_qmm_swiglu(x, gate, up, idx_dev(tok, dev), idx_dev(srt, dev), 64, 4)
+    assert h.dtype == torch.float32 and tuple(h.shape) == (tokens * k, 1, I)
+    xs = x.cpu().numpy().reshape(tokens, D)
+    hw = lambda t: (t[0].cpu().numpy().view(np.uint32), t[1].cpu().numpy(), t[2].cpu().numpy())
+    (gw, gs, gb), (uw, us, ub) = hw(gate), hw(up)
+    got = h.cpu().numpy().reshape(-1, I).astype(np.float64)
+    for r in (0, 5, 17, tokens * k - 1):
+        e, t = int(srt[r]), int(tok[r])
+        gg = O.qmm_f64(xs[t:t + 1], O.F32, gw[e], gs[e], gb[e], O.F32, 64, 4)
+        uu = O.qmm_f64(xs[t:t + 1], O.F32, uw[e], us[e], ub[e], O.F32, 64, 4)
+        ref = gg / (1 + np.exp(-gg)) * uu
+        assert rel_err(got[r:r + 1], ref) <= 1e-3, r

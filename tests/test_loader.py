@@ -121,3 +121,45 @@ def test_checkpoint_rejects_mismatched_bits(tmp_path):
     ck = loader.Checkpoint(d, "cpu")
     with pytest.raises(loader.CheckpointError, match="disagree"):
         ck.linear("model.layers.0.mlp.gate")
+
+
+@pytest.mark.parametrize("inner", [False, True])
+def test_checkpoint_loads_linear_bias(tmp_path, inner):
+    """Qwen2-style q/k/v biases (transformer.rs:180-191) load as QLinear.bias
+    from <layer>.bias or, after the remap, <layer>.inner.bias (lib.rs:1002-1005);
+    layers without one keep bias None."""
+    d = str(tmp_path)
+    q = "model.layers.0.self_attn.q_proj"
+    written = write_checkpoint(d, inner=inner, bias_layers=(q,))
+    ck = loader.Checkpoint(d, "cpu")
+    lin = ck.linear(q)
+    assert lin.bias is not None and lin.bias.dtype == torch.bfloat16
+    np.testing.assert_array_equal(lin.bias.view(torch.int16).numpy().view(np.uint16),
+                                  written[q + ".bias"])
+    assert ck.linear("model.layers.0.mlp.up_proj").bias is None
+
+
+def test_checkpoint_rejects_bias_of_wrong_length(tmp_path):
+    d = str(tmp_path)
+    q = "model.layers.0.self_attn.q_proj"
+    write_checkpoint(d, bias_layers=(q,))
+    ck = loader.Checkpoint(d, "cpu")
+    ck.tensors[q + ".bias"] = ck.tensors[q + ".bias"][:5]
+    with pytest.raises(loader.CheckpointError, match="is not"):
+        ck.linear(q)
+
+
+def test_prefixed_checkpoint_reads_override_under_the_full_key(tmp_path):
+    """With a prefix (a multimodal checkpoint's language model), the per-layer
+    override is keyed by the full tensor path (qwen3_next.rs:3431-3437 reads
+    'language_model.model.layers.0.mlp.gate'): the 8-bit router gate must get
+    its 8 bits, not the 4-bit default."""
+    d = str(tmp_path)
+    pre = "language_model."
+    written = write_checkpoint(d, prefix=pre)
+    ck = loader.Checkpoint(d, "cpu", prefix=pre)
+    gate = ck.linear("model.layers.0.mlp.gate")
+    assert (gate.group_size, gate.bits) == (64, 8)
+    np.testing.assert_array_equal(gate.weight.numpy().view(np.uint32),
+                                  written["model.layers.0.mlp.gate"][0])
+    assert ck.linear("model.layers.0.mlp.up_proj").bits == 4

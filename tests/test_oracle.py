@@ -345,3 +345,137 @@ def test_moe_combine_out_of_range_inv_gives_nan(orc):
     sc = np.full((4, 2), 0x3F80, np.uint16)
     out = gen.bf16_bits_to_f32(orc.moe_combine(y, O.BF16, inv, sc, O.BF16))
     assert np.isnan(out[2]).all() and not np.isnan(np.delete(out, 2, 0)).any()
+
+
+# --- quantize (mlx-rs ops::quantize, qwen3_next.rs:4305-4307, 12942) --------
+# MLX's exact scale selection cannot be checked offline (MLX is absent); the
+# oracle's quantize is pinned by what the algorithm's mathematics fixes:
+# exact recovery of inputs on a grid whose zero is a code, the negation and
+# power-of-two symmetries, the error bound, the code range and constant
+# groups. Each fails for a plausible slip (wrong n_bins, wrong edge or sign,
+# bias not the edge, a missing clip).
+
+def _qdeq64(wq, s, b, g, bits, dt):
+    q = O.unpack(wq, bits).astype(np.float64)
+    sf = (s if dt == O.F32 else O.to_f32(s, dt)).astype(np.float64)
+    bf = (b if dt == O.F32 else O.to_f32(b, dt)).astype(np.float64)
+    return q * np.repeat(sf, g, axis=-1) + np.repeat(bf, g, axis=-1)
+
+
+def _grid_rows(rng, rows, K, bits, g, zero_point=True):
+    """Rows of groups w = s0 * (q - z) with q spanning 0..n_bins in every group,
+    s0 a power of two and z an integer zero point (so 0 is a grid value)."""
+    nb = (1 << bits) - 1
+    q = rng.integers(0, nb + 1, (rows, K))
+    q[:, ::g] = 0
+    q[:, 1::g] = nb                              # both ends present in every group
+    z = rng.integers(0, nb + 1, (rows, K // g))
+    s0 = 2.0 ** rng.integers(-9, -2, (rows, K // g))
+    if not zero_point:
+        z = z + 0.5
+    return ((q - np.repeat(z, g, axis=1)) * np.repeat(s0, g, axis=1)).astype(np.float32)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("g", GROUPS)
+def test_quantize_recovers_grid_inputs_exactly(orc, bits, g):
+    rng = np.random.default_rng(bits * 1000 + g)
+    w = _grid_rows(rng, 6, 2 * 128, bits, g)
+    for dt in (O.F32, O.BF16, O.F16):
+        if dt == O.BF16 and bits == 8:
+            continue  # integers up to 255 times a power of two need 8 significant bits
+        wd = w if dt == O.F32 else O.from_f32(w, dt)
+        assert np.array_equal(O.to_f32(wd, dt) if dt != O.F32 else wd, w)
+        wq, s, b = O.quantize(wd, dt, g, bits)
+        assert np.array_equal(_qdeq64(wq, s, b, g, bits, dt), w.astype(np.float64)), (bits, g, dt)
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_quantize_error_bound_and_code_range(orc, bits):
+    rng = np.random.default_rng(7 + bits)
+    g = 64
+    w = (rng.standard_normal((8, 512)) * np.exp(rng.uniform(-6, 3, (8, 1)))).astype(np.float32)
+    w[0, :64] += 5.0                              # an all-positive group
+    w[1, :64] = -np.abs(w[1, :64]) - 1.0          # an all-negative group
+    wq, s, b = O.quantize(w, O.F32, g, bits)
+    q = O.unpack(wq, bits)
+    assert q.max() <= (1 << bits) - 1
+    err = np.abs(_qdeq64(wq, s, b, g, bits, O.F32) - w)
+    srep = np.abs(np.repeat(s.astype(np.float64), g, axis=1))
+    # every element within one step; elements that need no clip within half a
+    # step (+ float32 slack); the edge maps to an exact code
+    assert (err <= srep * (1 + 1e-5) + 1e-6 * np.abs(w)).all()
+    t = (w.astype(np.float64) - np.repeat(b, g, axis=1)) / np.repeat(s, g, axis=1)
+    inside = t <= (1 << bits) - 1 + 0.5 - 1e-3
+    assert (err[inside] <= 0.5 * srep[inside] * (1 + 1e-4) + 1e-6 * np.abs(w[inside])).all()
+    # a dropped clip or a wrong n_bins pushes far more than a few elements over
+    assert (~inside).sum() <= 2 * w.size // g
+
+
+def test_quantize_negation_and_power_of_two_symmetry(orc):
+    rng = np.random.default_rng(3)
+    w = rng.standard_normal((16, 256)).astype(np.float32)
+    for bits in (3, 4, 8):
+        wq, s, b = O.quantize(w, O.F32, 64, bits)
+        # negation: same codes, negated scales and biases (no |min| == |max| ties here)
+        wq2, s2, b2 = O.quantize(-w, O.F32, 64, bits)
+        assert np.array_equal(wq, wq2) and np.array_equal(s2, -s) and np.array_equal(b2, -b)
+        # power-of-two scaling is exact in every operation
+        wq3, s3, b3 = O.quantize(w * np.float32(8.0), O.F32, 64, bits)
+        assert np.array_equal(wq, wq3) and np.array_equal(s3, 8 * s) and np.array_equal(b3, 8 * b)
+
+
+def test_quantize_picks_the_larger_magnitude_edge(orc):
+    """The bias is the min or max of larger magnitude and the scale's sign
+    follows: a mostly-negative group keeps a positive scale and its minimum as
+    bias; a mostly-positive one a negative scale and its maximum."""
+    w = np.zeros((1, 64), np.float32)
+    w[0, :] = np.linspace(-3.0, 1.0, 64, dtype=np.float32)
+    wq, s, b = O.quantize(w, O.F32, 64, 4)
+    assert s[0, 0] > 0 and b[0, 0] == np.float32(-3.0)
+    wq, s, b = O.quantize(-w, O.F32, 64, 4)
+    assert s[0, 0] < 0 and b[0, 0] == np.float32(3.0)
+    assert O.unpack(wq, 4)[0, 0] == 0  # the edge itself is code 0
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16])
+def test_quantize_constant_and_zero_groups(orc, dt):
+    vals = np.array([0.0, 1.0, -2.5, 0.0078125, 1000.0, -0.001], np.float32)
+    w = np.repeat(vals, 64)[None, :]
+    wd = w if dt == O.F32 else O.from_f32(w, dt)
+    wq, s, b = O.quantize(wd, dt, 64, 4)
+    assert (O.unpack(wq, 4) == 0).all()
+    deq = _qdeq64(wq, s, b, 64, 4, dt)
+    ref = O.to_f32(wd, dt) if dt != O.F32 else wd
+    assert np.array_equal(deq, ref.astype(np.float64))
+
+
+def test_quantize_bf16_stays_within_its_rounding(orc):
+    """bf16 weights: scales and biases round to bf16, so the bound widens by
+    the rounding of the stored scale and bias (relative 2^-8 each)."""
+    rng = np.random.default_rng(11)
+    w = O.from_f32(rng.standard_normal((8, 256)).astype(np.float32), O.BF16)
+    wq, s, b = O.quantize(w, O.BF16, 64, 4)
+    wf = O.to_f32(w, O.BF16).astype(np.float64)
+    err = np.abs(_qdeq64(wq, s, b, 64, 4, O.BF16) - wf)
+    sr = np.abs(np.repeat(O.to_f32(s, O.BF16).astype(np.float64), 64, axis=1))
+    br = np.abs(np.repeat(O.to_f32(b, O.BF16).astype(np.float64), 64, axis=1))
+    assert (err <= sr * (1 + 15 * 2 ** -8) + br * 2 ** -8 + 1e-6).all()
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_quantize_represents_zero(orc, bits):
+    """The larger-magnitude edge is an exact multiple of the scale (scale =
+    edge / round(edge / scale)), so a 0 in a group maps to an integer code and
+    dequantizes to 0 up to float32 rounding (~n_bins * 2^-23 of a step);
+    keeping range / n_bins as the scale would miss 0 by up to half a step."""
+    rng = np.random.default_rng(19 + bits)
+    w = (rng.standard_normal((32, 256)) + rng.uniform(-2, 2, (32, 1))).astype(np.float32)
+    zeros = rng.integers(0, 64, (32, 4)) + np.arange(4) * 64
+    for r in range(32):
+        w[r, zeros[r]] = 0.0
+    wq, s, b = O.quantize(w, O.F32, 64, bits)
+    deq = _qdeq64(wq, s, b, 64, bits, O.F32)
+    srep = np.abs(np.repeat(s.astype(np.float64), 64, axis=1))
+    at0 = w == 0.0
+    assert (np.abs(deq[at0]) <= 1e-4 * srep[at0]).all()
