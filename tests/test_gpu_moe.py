@@ -215,3 +215,47 @@ def test_gather_qmm_swiglu_float32_activations_fall_back(dev):
         uu = O.qmm_f64(xs[t:t + 1], O.F32, uw[e], us[e], ub[e], O.F32, 64, 4)
         ref = gg / (1 + np.exp(-gg)) * uu
         assert rel_err(got[r:r + 1], ref) <= 1e-3, r
+
+
+@pytest.mark.parametrize("dt,g", [(O.BF16, 64), (O.F16, 64), (O.BF16, 128), (O.F16, 128)])
+def test_grouped_kernel_skewed_routing(dev, dt, g):
+    """4-bit sorted gather at groups 64 and 128 with skewed expert loads --
+    one expert with 150 rows (several row tiles over its weights), experts
+    with none, a 1-row expert, an out-of-range tail -- with x gathered
+    through lhs_indices, against the oracle on every row; and the fused
+    gate/up SwiGLU form over the same routing."""
+    from helpers import TORCH_DT, quant, to_dev, words_dev, x_of
+
+    Ex, N, K = 6, 192, 768
+    counts = [0, 150, 1, 0, 37, 19]
+    rhs = np.concatenate([np.full(c, e, np.uint32) for e, c in enumerate(counts)] +
+                         [np.array([Ex, Ex + 3], np.uint32)])
+    rows = len(rhs)
+    x = x_of(110 + g, (64, 1, K), dt)
+    lhs = np.random.default_rng(g).integers(0, 64, rows).astype(np.uint32)
+    lhs[5] = 999                                  # out-of-range x index -> NaN row
+    w, s, b = quant(111, Ex * N, K, 4, g, dt)
+    w, s, b = w.reshape(Ex, N, -1), s.reshape(Ex, N, -1), b.reshape(Ex, N, -1)
+    X = to_dev(x, dt, dev)
+    W, S, B = words_dev(w, dev), to_dev(s, dt, dev), to_dev(b, dt, dev)
+    y = ops.gather_qmm(X, W, S, B, idx_dev(lhs, dev), idx_dev(rhs, dev), True, g, 4, True)
+    got = y.float().cpu().numpy().reshape(rows, N).astype(np.float64)
+    ref = O.gather_qmm_f64(x, dt, w, s, b, dt, lhs, rhs, 1, N, K, g, 4, x_batch=64)
+    ref = ref.reshape(rows, N)
+    nan_rows = np.isnan(ref).any(axis=1)
+    assert nan_rows.sum() == 3 and np.array_equal(np.isnan(got).all(axis=1), nan_rows)
+    assert rel_err(got[~nan_rows], ref[~nan_rows]) <= 1e-2
+    # fused gate/up + SwiGLU over the same routing (the up weights: another seed)
+    wu, su, bu = quant(112, Ex * N, K, 4, g, dt)
+    wu, su, bu = wu.reshape(Ex, N, -1), su.reshape(Ex, N, -1), bu.reshape(Ex, N, -1)
+    h = ops.gather_qmm_swiglu(X, (W, S, B), (words_dev(wu, dev), to_dev(su, dt, dev),
+                                              to_dev(bu, dt, dev)),
+                              idx_dev(lhs, dev), idx_dev(rhs, dev), g, 4)
+    gh = h.float().cpu().numpy().reshape(rows, N).astype(np.float64)
+    ru = O.gather_qmm_f64(x, dt, wu, su, bu, dt, lhs, rhs, 1, N, K, g, 4, x_batch=64)
+    ru = ru.reshape(rows, N)
+    rg = O.to_f32(O.from_f32(ref.astype(np.float32), dt), dt).astype(np.float64)
+    ru = O.to_f32(O.from_f32(ru.astype(np.float32), dt), dt).astype(np.float64)
+    sw = rg / (1 + np.exp(-rg)) * ru
+    assert np.array_equal(np.isnan(gh).all(axis=1), nan_rows)
+    assert rel_err(gh[~nan_rows], sw[~nan_rows]) <= 1e-2
