@@ -24,7 +24,7 @@ INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 BITS = (2, 3, 4, 5, 6, 8)
-PER_BITS = ("hq_dequant.hip", "hq_qmv.hip", "hq_qmvx.hip", "hq_qmm.hip")
+PER_BITS = ("hq_dequant.hip", "hq_qmv.hip", "hq_qmvx.hip", "hq_qmm.hip", "hq_gqms.hip")
 ONCE = ("hq_capi.hip", "hq_moe.hip", "hq_quant.hip", "hq_device.hip")
 
 # -packed-fp32-ops off: hipcc must not form packed fp32 add/mul/fma, whose

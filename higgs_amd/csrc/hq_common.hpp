@@ -156,4 +156,24 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ int ilog2(int v) { return 31 - __clz(v); }
 
+// First index i in [0, n) with v[i] >= key (n if none), for non-decreasing v.
+// Wave-uniform result; two or three rounds of 64 probes for n <= 2^18.
+__device__ __forceinline__ int64_t wave_lower_bound(const uint32_t* v, int64_t n, uint32_t key) {
+  const int lane = threadIdx.x & 63;
+  int64_t lo = 0, hi = n;  // v[j] < key for j < lo; answer in [lo, hi]
+  while (lo < hi) {
+    const int64_t step = (hi - lo + 63) / 64;
+    const int64_t p = lo + (int64_t)lane * step;
+    const bool less = p < hi && v[p] < key;
+    const int c = __popcll(__ballot(less));  // probes below key form a prefix
+    if (c == 0) return lo;                  // v[lo] >= key
+    const int64_t nlo = lo + (int64_t)(c - 1) * step + 1;
+    const int64_t nhi = min(hi, lo + (int64_t)c * step);
+    if (step == 1) return nhi;
+    lo = nlo;
+    hi = nhi;
+  }
+  return lo;
+}
+
 }  // namespace hq

@@ -1,0 +1,466 @@
+// hq_gqms.hip -- sorted-expert grouped quantized matmul, streaming form, for
+// 4-bit weights: gather_qmm with sorted rhs indices (the MoE expert GEMM of
+// crates/higgs-models/src/qwen3_next.rs:1764-1799, FFI at 509-578) when each
+// expert has few routed rows and K <= 1024, as in the MoE down projection.
+//
+// y[r, n] = sum_k x[xi(r), k] * (s[e, n, g] * q[e, n, k] + b[e, n, g]),
+// e = rhs[r / M] (non-decreasing), g = k / group_size.
+//
+// Why a second grouped kernel: with ~32 rows per expert (configs[4]: 4096
+// routed rows over 128 experts) the LDS-dequantizing GEMM dequantizes every W
+// tile for few rows. Here the matrix cores take the packed nibbles as
+// (OFF + q) bf16/fp16 operands with no dequantization, and the per-group scale
+// and bias are applied to the fp32 partial sums:
+//   acc += s * D_g + (b - OFF * s) * X_g,   X_g = sum of x over the group.
+//
+// Layout of one v_mfma_f32_16x16x32 step: B = 16 W rows (lane n = lane % 16)
+// x 32 k, A = 16 x rows, D[m, n]. For every MFMA step to stay inside one
+// scale group, lane group q = lane / 16 loads words [q*WPG, q*WPG + WPG) of
+// each group (WPG = group_size / 32 words), and step t of the group uses word
+// t: elements g*GS + q*GS/4 + 8t + (0..7), the unpack giving the pairs
+// (j, j + 4); x sits in LDS in that pair order (0,4,1,5,2,6,3,7) per
+// 8-element block.
+//
+// Block (tile range, e): 8 waves. The block finds the run of rows routed to
+// e by a wave-wide search over the sorted indices (unused experts cost no
+// weight traffic), loads up to 64 of those rows of x for the whole K straight
+// into LDS (global_load_lds_dwordx4), computes the group sums (v_dot2 against
+// ones) and reorders x to the pair order in place, then each wave streams its
+// 16-row W tiles through a register double buffer while it multiplies. The
+// block row e == w_batch fills rows of out-of-range expert indices with NaN,
+// and rows whose x index is out of range are NaN too.
+#include <atomic>
+#include <type_traits>
+
+#include "hq_common.hpp"
+#include "hq_device.hpp"
+#include "hq_kernels.hpp"
+
+#ifndef HQ_BITS
+#error "compile with -DHQ_BITS=<2|3|4|5|6|8>"
+#endif
+
+namespace hq {
+
+namespace {
+
+struct GSKern {
+  void* y;
+  const void* x;
+  const uint32_t* w;
+  const void* s;
+  const void* b;
+  const uint32_t* lhs;
+  const uint32_t* rhs;
+  int64_t batch, x_rep, x_batch, w_batch;
+  int M, N, K;
+  uint32_t nib_mask, off_pair;  // 0x000F000F and the (OFF, OFF) pair, kept out of literals
+  int ntiles;                   // 16-column output tiles: ceil(N / 16)
+  int ns;                       // blocks splitting the tiles (grid.x)
+};
+
+template <int XDT> struct SMma;
+template <> struct SMma<DT_BF16> {
+  using frag = bf16x8;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static constexpr uint32_t OFFB = 0x43004300u;  // (128 + q) for q < 128
+  static constexpr float OFF = 128.f;
+  static constexpr uint32_t ONE2 = 0x3F803F80u;
+};
+template <> struct SMma<DT_F16> {
+  using frag = f16x8;
+  static __device__ __forceinline__ floatx4 mma(frag a, frag b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static constexpr uint32_t OFFB = 0x64006400u;  // (1024 + q) for q < 1024
+  static constexpr float OFF = 1024.f;
+  static constexpr uint32_t ONE2 = 0x3C003C00u;
+};
+
+// 16 (4) bytes per lane from global memory straight into LDS at
+// lds_wave + 16 * lane (4 * lane); lds_wave is wave-uniform.
+__device__ __forceinline__ void dma16(const void* g, void* lds_wave) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
+                                   (void __attribute__((address_space(3)))*)lds_wave, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* lds_wave) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
+                                   (void __attribute__((address_space(3)))*)lds_wave, 4, 0, 0);
+}
+
+// s_waitcnt immediate (gfx9 encoding): at most `vm` vector memory operations
+// outstanding, every LDS operation complete.
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+
+constexpr int kMR = 64;  // x rows per block pass (four 16-row MFMA tiles)
+// LDS of one block: group sums, the out-of-range flags, x rows of K + 8 elements.
+template <int GS, int K>
+constexpr int gx_lds_bytes() { return (K / GS) * kMR * 4 + kMR * 4 + kMR * (K + 8) * 2; }
+
+template <int XDT, int GS, int KC>
+__global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
+  constexpr int KK = KC * 256;
+  constexpr int G = KK / GS;        // scale groups per W row
+  constexpr int NGC = 256 / GS;     // groups per 256-element chunk
+  constexpr int WPG = GS / 32;      // words per lane per group (2 or 4)
+  constexpr int XLD = KK + 8;       // LDS row stride of x in elements (2K + 16 bytes:
+                                    // 16 lanes reading 16 B of 16 rows hit 16 bank groups)
+  constexpr int MR = kMR;
+  constexpr int RPW = MR / 8;       // x rows each of the 8 waves stages
+  // An item is one K part (CP chunks of 256) of one 16-row W tile: at most 4
+  // chunks (32 words per lane), so two items in flight fit the registers.
+  constexpr int CP = KC % 4 == 0 ? 4 : (KC % 3 == 0 ? 3 : KC);
+  constexpr int KP = KC / CP;       // parts per tile
+  constexpr int GP = G / KP;        // groups per part
+  constexpr int WPP = GP / 2;       // scale words per part
+  constexpr int SW = (WPP + 3) / 4; // scale words each lane group q holds
+  constexpr int NWL = CP * NGC;     // weight load instructions per item
+  static_assert(WPG == 2 || WPG == 4, "group size 64 or 128");
+  static_assert(GP % 2 == 0 && KC % CP == 0, "whole scale words per part");
+  static_assert(gx_lds_bytes<GS, KK>() <= 160 * 1024, "x rows fit the LDS");
+  using T = SMma<XDT>;
+  using frag = typename T::frag;
+  using XS = st_t<XDT>;
+
+  // the small arrays first, so every group-sum read folds its offset into
+  // the instruction (LDS offsets stop at 64 KB)
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* Xs = reinterpret_cast<float*>(smem);                              // [G][MR] group sums
+  int* xbad = reinterpret_cast<int*>(smem + G * MR * 4);                   // [MR]
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + G * MR * 4 + MR * 4);  // [MR][XLD]
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nl = lane & 15, q = lane >> 4;
+  const int N = a.N, M = a.M;
+  const int64_t e = blockIdx.y;
+  const int tpb = (a.ntiles + a.ns - 1) / a.ns;
+  const int tb = blockIdx.x * tpb, te = min(a.ntiles, tb + tpb);
+  if (tb >= te) return;
+  const bool expert_ok = e < a.w_batch;
+  const int64_t s0 = wave_lower_bound(a.rhs, a.batch, (uint32_t)e);
+  const int64_t s1 = expert_ok ? wave_lower_bound(a.rhs, a.batch, (uint32_t)(e + 1)) : a.batch;
+  const int64_t r_begin = s0 * M, r_end = s1 * M;  // flattened (element, m) rows
+  if (r_begin >= r_end) return;  // block-uniform
+  XS* yg = (XS*)a.y;
+  constexpr uint16_t kNaN = XDT == DT_BF16 ? 0x7fc0u : 0x7e00u;
+  if (!expert_ok) {
+    const int c0 = tb * 16, c1 = min(te * 16, N);
+    for (int64_t r = r_begin; r < r_end; r++)
+      for (int n = c0 + tid; n < c1; n += 512) yg[r * N + n] = kNaN;
+    return;
+  }
+
+  // this wave's tiles: tb + wv + 8j; item i = j * KP + part
+  const int ntw = max(0, (te - tb - wv + 7) / 8);
+  const int NI = ntw * KP;
+  const int64_t P = KK / 8;  // words per W row
+
+  struct Buf {
+    uint32_t wd[CP][8];
+    uint32_t sv[SW], bv[SW];  // scale / bias words q*SW .. of the part
+  };
+  // row of W and part of item i (clamped to the last item: loads past the end
+  // reload it and are never computed)
+  auto item_at = [&](int i, int& part) __attribute__((always_inline)) -> int64_t {
+    const int ii = min(i, max(NI - 1, 0));
+    part = ii % KP;
+    const int t = min(tb + wv + 8 * (ii / KP), te - 1);
+    return e * N + min(t * 16 + nl, N - 1);
+  };
+  auto issue_sb = [&](Buf& b, int i) __attribute__((always_inline)) {
+    int part;
+    const int64_t row = item_at(i, part);
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>((const XS*)a.s + row * G) + part * WPP;
+    const uint32_t* bp = reinterpret_cast<const uint32_t*>((const XS*)a.b + row * G) + part * WPP;
+    if constexpr (SW * 4 == WPP && SW == 2) {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(sp + q * 2), u = *reinterpret_cast<const u32x2*>(bp + q * 2);
+      b.sv[0] = v[0]; b.sv[1] = v[1]; b.bv[0] = u[0]; b.bv[1] = u[1];
+    } else if constexpr (SW * 4 == WPP && SW == 4) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(sp + q * 4), u = *reinterpret_cast<const u32x4*>(bp + q * 4);
+#pragma unroll
+      for (int j = 0; j < 4; j++) { b.sv[j] = v[j]; b.bv[j] = u[j]; }
+    } else {  // words past the part are clamped (never used)
+#pragma unroll
+      for (int j = 0; j < SW; j++) {
+        const int wi = min(q * SW + j, WPP - 1);
+        b.sv[j] = sp[wi];
+        b.bv[j] = bp[wi];
+      }
+    }
+  };
+  auto issue_w = [&](Buf& b, int i) __attribute__((always_inline)) {
+    int part;
+    const int64_t row = item_at(i, part);
+    const uint32_t* wp = a.w + row * P + part * (CP * 32) + q * WPG;
+#pragma unroll
+    for (int c = 0; c < CP; c++)
+#pragma unroll
+      for (int g = 0; g < NGC; g++) {
+        if constexpr (WPG == 2) {
+          const u32x2 v = *reinterpret_cast<const u32x2*>(wp + c * 32 + g * (GS / 8));
+          b.wd[c][2 * g] = v[0];
+          b.wd[c][2 * g + 1] = v[1];
+        } else {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(wp + c * 32 + g * (GS / 8));
+#pragma unroll
+          for (int t = 0; t < 4; t++) b.wd[c][4 * g + t] = v[t];
+        }
+      }
+  };
+
+  const uint32_t mask_s = a.nib_mask;
+  uint32_t off_v;
+  asm("v_mov_b32 %0, %1" : "=v"(off_v) : "s"(a.off_pair));
+
+  Buf ba, bb;
+  for (int64_t r0 = r_begin; r0 < r_end; r0 += MR) {
+    const int nrows = (int)min((int64_t)MR, r_end - r0);
+    // x row offsets of this wave's rows (token gather through lhs)
+    int64_t xoff[RPW];
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+      const int rr = wv + 8 * k;
+      const int64_t r = r0 + min(rr, nrows - 1);
+      const int64_t bi = M == 1 ? r : r / M;
+      const int64_t xi = a.lhs ? (int64_t)a.lhs[bi] : bi / a.x_rep;
+      xoff[k] = (min(xi, a.x_batch - 1) * M + (r - bi * M)) * (int64_t)KK;
+      if (lane == 0 && rr < nrows) xbad[rr] = xi >= a.x_batch;
+    }
+    // The first item's scales, then x straight into LDS (every row slot of
+    // the pass; slots past the last row repeat it), then the first item's
+    // weights. The DMA code is branch-free, so the explicit wait below leaves
+    // exactly those NWL weight loads in flight while it covers every DMA
+    // (sched barriers keep the order; tests/test_capi.py checks the count in
+    // the compiled code).
+    issue_sb(ba, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+      const XS* src = (const XS*)a.x + xoff[k] + lane * 8;
+      uint16_t* dst = xs + (wv + 8 * k) * XLD;
+#pragma unroll
+      for (int p = 0; p < KK / 512; p++) dma16(src + p * 512, dst + p * 512);
+      if constexpr (KK % 512 != 0) {  // 256-element tail: two 4-byte pieces per lane
+        const XS* ts = (const XS*)a.x + xoff[k] + (KK / 512) * 512 + lane * 2;
+        dma4(ts, dst + (KK / 512) * 512);
+        dma4(ts + 128, dst + (KK / 512) * 512 + 128);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue_w(ba, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(NWL));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // group sums of x (v_dot2 against ones) and the in-place reorder of every
+    // 8-element block to the MFMA pair order (0,4,1,5,2,6,3,7); row-fastest
+    // thread order keeps the 16-byte LDS accesses free of bank conflicts
+    for (int idx = tid; idx < MR * G; idx += 512) {
+      const int row = idx % MR, g = idx / MR;
+      if (row < nrows) {
+        uint16_t* p = xs + row * XLD + g * GS;
+        float sum = 0.f;
+#pragma unroll
+        for (int pc = 0; pc < GS / 8; pc++) {
+          const u32x4 d = *reinterpret_cast<const u32x4*>(p + pc * 8);
+          // (the pairs are taken out by name: a bit_cast of d[j] inside a loop
+          // compiled to four reads of d[0])
+          const uint32_t d0 = d.x, d1 = d.y, d2 = d.z, d3 = d.w;
+          if constexpr (XDT == DT_BF16) {
+            typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+            const b2 one = __builtin_bit_cast(b2, 0x3F803F80u);
+            sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, d0), one, sum, false);
+            sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, d1), one, sum, false);
+            sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, d2), one, sum, false);
+            sum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, d3), one, sum, false);
+          } else {
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            const h2 one = __builtin_bit_cast(h2, 0x3C003C00u);
+            sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, d0), one, sum, false);
+            sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, d1), one, sum, false);
+            sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, d2), one, sum, false);
+            sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, d3), one, sum, false);
+          }
+          u32x4 o;
+          o[0] = (d[0] & 0xffffu) | (d[2] << 16);
+          o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
+          o[2] = (d[1] & 0xffffu) | (d[3] << 16);
+          o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
+          *reinterpret_cast<u32x4*>(p + pc * 8) = o;
+        }
+        Xs[g * MR + row] = sum;
+      }
+    }
+    // LDS writes done; the weight loads stay in flight
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // items of MT active 16-row tiles, weights double-buffered in registers
+    auto run_items = [&](auto mt_c) __attribute__((always_inline)) {
+      constexpr int MT = decltype(mt_c)::value;
+      float acc[MT][4];
+      auto compute = [&](const Buf& b, int i) __attribute__((always_inline)) {
+        // x and its sums do not change across items: without this the
+        // compiler hoists every A-fragment read out of the item loop
+        asm volatile("" ::: "memory");
+        // lane coordinates opaque to the optimizer, so per-item addresses are
+        // recomputed per item instead of living across the loop
+        int qo = q, nlo = nl;
+        asm volatile("" : "+v"(qo), "+v"(nlo));
+        const int part = i % KP;
+        if (part == 0) {
+#pragma unroll
+          for (int j = 0; j < MT; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[j][v] = 0.f;
+        }
+        const uint16_t* xrow = xs + nlo * XLD + part * (CP * 256) + qo * (GS / 4);
+        const float* xsum = Xs + part * GP * MR + 4 * qo;
+#pragma unroll
+        for (int c = 0; c < CP; c++)
+#pragma unroll
+          for (int g = 0; g < NGC; g++) {
+            __builtin_amdgcn_sched_barrier(0);  // one group at a time (bounded live registers)
+            floatx4 D[MT];
+#pragma unroll
+            for (int j = 0; j < MT; j++) D[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < WPG; t++) {
+              const uint32_t w = b.wd[c][g * WPG + t];
+              u32x4 bw;
+              bw[0] = (w & mask_s) | off_v;
+              bw[1] = ((w >> 4) & mask_s) | off_v;
+              bw[2] = ((w >> 8) & mask_s) | off_v;
+              bw[3] = ((w >> 12) & mask_s) | off_v;
+#pragma unroll
+              for (int j = 0; j < MT; j++) {
+                const u32x4 av = *reinterpret_cast<const u32x4*>(xrow + 16 * j * XLD + c * 256 + g * GS + 8 * t);
+                D[j] = T::mma(__builtin_bit_cast(frag, av), __builtin_bit_cast(frag, bw), D[j]);
+              }
+            }
+            const int gl = c * NGC + g;  // group within the part
+            const int wi = gl / 2, owner = wi / SW, sl = wi % SW;
+            const uint32_t swd = __shfl(b.sv[sl], nlo + 16 * owner, 64);
+            const uint32_t bwd = __shfl(b.bv[sl], nlo + 16 * owner, 64);
+            const float sv = DT_<XDT>::to_f32((uint16_t)((swd >> (16 * (gl & 1))) & 0xffffu));
+            const float bo = fmaf(-T::OFF, sv, DT_<XDT>::to_f32((uint16_t)((bwd >> (16 * (gl & 1))) & 0xffffu)));
+#pragma unroll
+            for (int j = 0; j < MT; j++) {
+              const floatx4 X = *reinterpret_cast<const floatx4*>(xsum + gl * MR + 16 * j);
+#pragma unroll
+              for (int v = 0; v < 4; v++) {
+                acc[j][v] = fmaf(sv, D[j][v], fmaf(bo, X[v], acc[j][v]));
+                // pin the group's epilogue here: left free, the compiler
+                // sinks every group's FMAs below all the MFMAs and keeps
+                // each group's partial sums live (hundreds of registers)
+                asm volatile("" : "+v"(acc[j][v]));
+              }
+            }
+          }
+        if (part != KP - 1) return;
+        // acc[j][v] = y[row 16j + 4q + v][column t*16 + nl]
+        const int t = tb + wv + 8 * (i / KP);
+        const int col = t * 16 + nlo;
+        if (col >= N) return;
+        XS* yp = yg + (r0 + 4 * qo) * N + col;  // row 4q of the pass
+#pragma unroll
+        for (int j = 0; j < MT; j++)
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            const int m = 16 * j + 4 * qo + v;
+            if (m < nrows) {
+              yp[(int64_t)(16 * j + v) * N] = xbad[m] ? kNaN : DT_<XDT>::from_f32(acc[j][v]);
+            }
+          }
+      };
+      // loads stay out of branches (clamped item indices past the end reload
+      // the last item, never computed), so each wait covers only older loads
+#pragma nounroll
+      for (int i = 0; i < NI; i += 2) {
+        issue_sb(bb, i + 1);
+        issue_w(bb, i + 1);
+        compute(ba, i);
+        issue_sb(ba, i + 2);
+        issue_w(ba, i + 2);
+        if (i + 1 < NI) compute(bb, i + 1);
+      }
+    };
+    const int mt = (nrows + 15) / 16;
+    if (mt == 1) run_items(std::integral_constant<int, 1>{});
+    else if (mt == 2) run_items(std::integral_constant<int, 2>{});
+    else if (mt == 3) run_items(std::integral_constant<int, 3>{});
+    else run_items(std::integral_constant<int, 4>{});
+    __syncthreads();  // x, its sums and xbad are rewritten by the next pass
+  }
+}
+
+template <int XDT, int GS, int KC>
+hipError_t run_gqms(const QArgs& a) {
+  constexpr int lds = gx_lds_bytes<GS, KC * 256>();
+  GSKern k;
+  k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b; k.lhs = a.lhs; k.rhs = a.rhs;
+  k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
+  k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
+  k.nib_mask = 0x000F000Fu;
+  k.off_pair = SMma<XDT>::OFFB;
+  k.ntiles = (int)((a.N + 15) / 16);
+  k.ns = (k.ntiles + 31) / 32;  // about 32 weight tiles (16 rows x K) per block
+  auto fn = gqms_kernel<XDT, GS, KC>;
+  static std::atomic<uint64_t> raised{0};
+  hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), lds, raised);
+  if (e != hipSuccess) return e;
+  dim3 grid((unsigned)k.ns, (unsigned)(a.w_batch + 1));
+  hipLaunchKernelGGL(fn, grid, dim3(512), lds, a.stream, k);
+  return hipGetLastError();
+}
+
+template <int XDT, int GS>
+hipError_t run_gqms_k(const QArgs& a) {
+  switch (a.K / 256) {
+    case 2: return run_gqms<XDT, GS, 2>(a);
+    case 3: if constexpr (GS == 64) return run_gqms<XDT, GS, 3>(a); else break;
+    case 4: return run_gqms<XDT, GS, 4>(a);
+    default: break;
+  }
+  return hipErrorNotSupported;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+#define HQ_CAT_(a, b) a##b
+#define HQ_CAT(a, b) HQ_CAT_(a, b)
+
+// The streaming grouped kernel, or hipErrorNotSupported for what it does not
+// take: other bit widths, group size 32, mixed or fp32 dtypes, K not one of
+// 512/768/1024 (768 only at group size 64), the fused SwiGLU, scales or
+// biases not 16-byte aligned, more than 64 rows per expert on average (the
+// LDS-dequant GEMM amortises its dequantization there).
+hipError_t HQ_CAT(launch_gqms_t_b, HQ_BITS)(const QArgs& a) {
+  if constexpr (HQ_BITS != 4) {
+    (void)a;
+    return hipErrorNotSupported;
+  } else {
+    // Measured at configs[4] (4096 rows, 128 experts): K = 768 66 us against
+    // the LDS-dequant kernel's 73. With K = 2048 (then only 32 x rows fit the
+    // LDS, and experts of 33-64 rows take two passes) it measured 84 against
+    // 76 us, and with the fused SwiGLU 141 against 80: the kernel is
+    // VALU-bound (13.6 VALU instructions per MFMA), so it takes the unfused
+    // single-pass case only.
+    if (a.w2 || a.xdt != a.sdt || a.xdt == DT_F32 || !a.rhs || a.w_batch + 1 > 65535)
+      return hipErrorNotSupported;
+    if (a.group_size != 64 && a.group_size != 128) return hipErrorNotSupported;
+    if (a.K % 256 != 0 || a.K > 1024 || a.M > ((int64_t)1 << 30)) return hipErrorNotSupported;
+    if (!aligned16(a.s) || !aligned16(a.b)) return hipErrorNotSupported;
+    if (a.batch * a.M > 64 * a.w_batch) return hipErrorNotSupported;  // few rows per expert
+    return a.xdt == DT_BF16 ? (a.group_size == 64 ? run_gqms_k<DT_BF16, 64>(a) : run_gqms_k<DT_BF16, 128>(a))
+                            : (a.group_size == 64 ? run_gqms_k<DT_F16, 64>(a) : run_gqms_k<DT_F16, 128>(a));
+  }
+}
+
+}  // namespace hq

@@ -664,25 +664,6 @@ struct GQKern {
   const void* b2;
 };
 
-// First index i in [0, n) with v[i] >= key (n if none), for non-decreasing v.
-// Wave-uniform result; two or three rounds of 64 probes for n <= 2^18.
-__device__ __forceinline__ int64_t wave_lower_bound(const uint32_t* v, int64_t n, uint32_t key) {
-  const int lane = threadIdx.x & 63;
-  int64_t lo = 0, hi = n;  // v[j] < key for j < lo; answer in [lo, hi]
-  while (lo < hi) {
-    const int64_t step = (hi - lo + 63) / 64;
-    const int64_t p = lo + (int64_t)lane * step;
-    const bool less = p < hi && v[p] < key;
-    const int c = __popcll(__ballot(less));  // probes below key form a prefix
-    if (c == 0) return lo;                  // v[lo] >= key
-    const int64_t nlo = lo + (int64_t)(c - 1) * step + 1;
-    const int64_t nhi = min(hi, lo + (int64_t)c * step);
-    if (step == 1) return nhi;
-    lo = nlo;
-    hi = nhi;
-  }
-  return lo;
-}
 
 // SWI: a tile's 128 W rows are 64 output columns of the gate and the same
 // columns of the up projection; wave wn's fragment 0 holds gate columns
@@ -906,6 +887,9 @@ hipError_t run_gqmm_g(const QArgs& a) {
 // Sorted-index gather_qmm through the grouped kernel, or hipErrorNotSupported
 // (dtype mix, K not a multiple of 64, too many experts for the grid).
 hipError_t HQ_CAT(launch_gqmm_t_b, HQ_BITS)(const QArgs& a) {
+  // few rows per expert: the streaming grouped kernel (hq_gqms.hip)
+  const hipError_t es = HQ_CAT(launch_gqms_t_b, HQ_BITS)(a);
+  if (es != hipErrorNotSupported) return es;
   if (a.xdt != a.sdt || a.xdt == DT_F32 || a.K % GBK != 0 || a.w_batch + 1 > 65535 || !a.rhs)
     return hipErrorNotSupported;
   return a.w2 ? run_gqmm_g<true>(a) : run_gqmm_g<false>(a);

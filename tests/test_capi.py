@@ -314,3 +314,45 @@ def test_switch_projection_settings():
     assert ops._proj((1, 2, 3, 32, 8), 64, 4) == ((1, 2, 3), 32, 8)
     with pytest.raises(HiggsQmmError):
         ops._proj((1, 2), 64, 4)
+
+
+
+def test_grouped_stream_kernel_waits_for_its_lds_dma():
+    """The streaming grouped kernel (hq_gqms.hip) loads x straight into LDS,
+    issues the first weight tile's loads behind it, and then waits with an
+    explicit vmcnt of exactly those weight loads before the barrier, so the
+    weights stay in flight. That is only correct if the code from the last LDS
+    DMA to the barrier is straight-line and holds that many vector-memory
+    instructions; check every instantiation in the compiled gfx950 assembly."""
+    import shutil
+    import subprocess
+    import tempfile
+
+    from higgs_amd import build as hb
+
+    if shutil.which(hb.HIPCC) is None and not os.path.exists(hb.HIPCC):
+        pytest.skip("hipcc not available")
+    with tempfile.TemporaryDirectory() as td:
+        asm = os.path.join(td, "gqms.s")
+        subprocess.run([hb.HIPCC, *hb.FLAGS, "-DHQ_BITS=4", "--cuda-device-only", "-S",
+                        os.path.join(hb.CSRC, "hq_gqms.hip"), "-o", asm],
+                       check=True, capture_output=True)
+        txt = open(asm).read()
+    kernels = re.split(r"\n(_ZN\S*gqms_kernel\S+):", txt)[1:]
+    assert kernels, "no gqms_kernel instantiation in the assembly"
+    vm_op = re.compile(r"^\s+(global_|buffer_|scratch_|flat_)")
+    for name, body in zip(kernels[0::2], kernels[1::2]):
+        lines = body.split("\n")
+        dmas = [i for i, ln in enumerate(lines) if "global_load_lds" in ln]
+        assert dmas, name
+        # the DMA block is one straight run ending in the waited barrier
+        last = dmas[-1]
+        bar = next(i for i in range(last, len(lines)) if re.match(r"^\s+s_barrier", lines[i]))
+        span = lines[dmas[0]:bar]
+        assert not any(re.match(r"^\S+:", ln) or re.match(r"^\s+s_(c)?branch", ln)
+                       for ln in span), name
+        between = [ln for ln in lines[last + 1:bar] if vm_op.match(ln)]
+        waits = [ln for ln in lines[last + 1:bar] if "s_waitcnt" in ln and "vmcnt" in ln]
+        assert waits, name
+        vm = int(re.search(r"vmcnt\((\d+)\)", waits[-1]).group(1))
+        assert vm == len(between) > 0, (name, vm, len(between))

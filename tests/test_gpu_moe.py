@@ -217,8 +217,9 @@ def test_gather_qmm_swiglu_float32_activations_fall_back(dev):
         assert rel_err(got[r:r + 1], ref) <= 1e-3, r
 
 
+@pytest.mark.parametrize("K", [768, 1024])
 @pytest.mark.parametrize("dt,g", [(O.BF16, 64), (O.F16, 64), (O.BF16, 128), (O.F16, 128)])
-def test_grouped_kernel_skewed_routing(dev, dt, g):
+def test_grouped_kernel_skewed_routing(dev, dt, g, K):
     """4-bit sorted gather at groups 64 and 128 with skewed expert loads --
     one expert with 150 rows (several row tiles over its weights), experts
     with none, a 1-row expert, an out-of-range tail -- with x gathered
@@ -226,7 +227,7 @@ def test_grouped_kernel_skewed_routing(dev, dt, g):
     gate/up SwiGLU form over the same routing."""
     from helpers import TORCH_DT, quant, to_dev, words_dev, x_of
 
-    Ex, N, K = 6, 192, 768
+    Ex, N = 6, 192
     counts = [0, 150, 1, 0, 37, 19]
     rhs = np.concatenate([np.full(c, e, np.uint32) for e, c in enumerate(counts)] +
                          [np.array([Ex, Ex + 3], np.uint32)])
