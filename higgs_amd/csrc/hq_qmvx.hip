@@ -121,6 +121,13 @@ __device__ __forceinline__ st_t<ODT> nanv() {
 
 constexpr int kU = 4;  // segments whose loads are issued together
 
+// Bytes of one x row in LDS: 16 more than the row, so that the same column of
+// consecutive rows falls in different LDS banks (rows of 128-element segments
+// are whole multiples of the 256-byte bank cycle; several x rows read one
+// column at a time measured 3.4 bank-conflict cycles per LDS cycle at 8 rows;
+// the step time did not change, LDS is not what limits those kernels).
+__host__ __device__ constexpr int xrow_bytes(int k) { return k * 2 + 16; }
+
 // BITS, x dtype (bf16 | fp16), scale dtype, MB = M rounded up to 1/2/4/8,
 // GS = group size.
 template <int BITS, int XDT, int SDT, int MB, int GS>
@@ -149,7 +156,7 @@ __global__ __launch_bounds__(1024) void qmvx_kernel(QXKern a) {
   // LDS: x rows [M + 1][KC] (row M is zeros), X sums [KC/GS][RPH] floats,
   // reduction slots [W][Z][M][16] floats.
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  float* Xs = reinterpret_cast<float*>(smem + (size_t)(M + 1) * KC * 2);
+  float* Xs = reinterpret_cast<float*>(smem + (size_t)(M + 1) * xrow_bytes(KC));
   float* red = Xs + (KC / GS) * RPH;
 
   const int nl = lane & 15, q = lane >> 4;
@@ -164,7 +171,7 @@ __global__ __launch_bounds__(1024) void qmvx_kernel(QXKern a) {
     const int m = mrow % RPH;
     const int hq = q * Z / 4;                       // half of this lane's k-block
     const bool valid = (h == hq) && (m < M) && (h < Z);
-    abase[mf] = (valid ? m : M) * KC * 2 + q * 64;
+    abase[mf] = (valid ? m : M) * xrow_bytes(KC) + q * 64;
   }
   // D-side: half and x-row of this lane's accumulator values, per MFMA.
   int dh[NMF];
@@ -218,7 +225,7 @@ __global__ __launch_bounds__(1024) void qmvx_kernel(QXKern a) {
           o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
           o[2] = (d[1] & 0xffffu) | (d[3] << 16);
           o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
-          *reinterpret_cast<u32x4*>(xs + (size_t)m * KC + c * 8) = o;
+          *reinterpret_cast<u32x4*>(smem + (size_t)m * xrow_bytes(KC) + c * 16) = o;
           // GS/8 consecutive threads hold one group: reduce in the wave.
 #pragma unroll
           for (int o2 = 1; o2 < GS / 8; o2 <<= 1) sum += __shfl_xor(sum, o2, 64);
@@ -421,7 +428,7 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
 
   // LDS: x rows [M][K] | 64 B of zeros | X sums [G][MB] | red [2][W][MB][16]
   // (| gate sums [MB][16] with SWI); with DX no x rows, zeros or X sums.
-  const int zoff = DX ? 0 : M * K * 2;
+  const int zoff = DX ? 0 : M * xrow_bytes(K);
   float* Xs = reinterpret_cast<float*>(smem + zoff + 64);
   float* red = DX ? reinterpret_cast<float*>(smem) : Xs + G * MB;
 
@@ -430,7 +437,7 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
   const int sigA = nl / MB, mA = nl % MB;
   const int uA = sigA / Z, hA = sigA % Z;
   const bool validA = (hA == q * Z / 4) && (mA < M) && (sigA < NSLOT);
-  const int xlane = mA * K * 2 + q * 64;
+  const int xlane = mA * xrow_bytes(K) + q * 64;
   // D side: values v = 0..3 of this lane are rows 4q + v.
   const int sig0 = (4 * q) / MB;          // slot of value 0
   const int gsig = sig0 < NSLOT ? sig0 : 0;  // clamped for loads
@@ -634,7 +641,7 @@ __global__ __launch_bounds__(512) void qmvp_kernel(PKern a) {
     o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
     o[2] = (d[1] & 0xffffu) | (d[3] << 16);
     o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
-    *reinterpret_cast<u32x4*>(smem + ((size_t)m * K + c * 8) * 2) = o;
+    *reinterpret_cast<u32x4*>(smem + (size_t)m * xrow_bytes(K) + c * 16) = o;
     // GS/8 consecutive lanes hold one group
 #pragma unroll
     for (int o2 = 1; o2 < GS / 8; o2 <<= 1) sum += __shfl_xor(sum, o2, 64);
@@ -743,7 +750,7 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
   const int64_t P = (int64_t)(K >> 5) * BITS;  // words per weight row
   const int G = K / GS;                        // groups per row
   // LDS: x [M][K] in pair order | 64 B of zeros | red [2][W][MB][16] floats
-  const int zoff = M * K * 2;
+  const int zoff = M * xrow_bytes(K);
   float* red = reinterpret_cast<float*>(smem + zoff + 64);
 
   const int nl = lane & 15, q = lane >> 4;
@@ -803,7 +810,7 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
     o[1] = (d[0] >> 16) | (d[2] & 0xffff0000u);
     o[2] = (d[1] & 0xffffu) | (d[3] << 16);
     o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
-    *reinterpret_cast<u32x4*>(smem + (size_t)m * K * 2 + seg0 * 256 + j * 16) = o;
+    *reinterpret_cast<u32x4*>(smem + (size_t)m * xrow_bytes(K) + seg0 * 256 + j * 16) = o;
   };
   u32x4 xr[XPRE > 0 ? XPRE : 1];
 #pragma unroll
@@ -820,7 +827,7 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
 
   constexpr uint32_t ONE2 = XDT == DT_BF16 ? 0x3F803F80u : 0x3C003C00u;
   const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
-  const int xrowA = (validA ? mA : 0) * K * 2;
+  const int xrowA = (validA ? mA : 0) * xrow_bytes(K);
 
   // Adds one item (K range starting at segment seg_base) to the 4 values per
   // lane.
@@ -991,7 +998,7 @@ hipError_t run_qmvs(const QArgs& a) {
   const int W = (int)(a.K / (128 * S * RW));
   if (a.K % (128 * S * RW) != 0 || W < 2 || W > 8 || a.M > MB) return hipErrorNotSupported;
   if (kXPre<MB, S> && a.M != MB) return hipErrorNotSupported;
-  const size_t lds = (size_t)a.M * a.K * 2 + 64 + (size_t)2 * W * MB * 16 * 4;
+  const size_t lds = (size_t)a.M * xrow_bytes((int)a.K) + 64 + (size_t)2 * W * MB * 16 * 4;
   if (lds > 160 * 1024) return hipErrorNotSupported;
   SKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
@@ -1016,7 +1023,7 @@ hipError_t run_qmvs(const QArgs& a) {
 inline size_t qmvp_lds(const QArgs& a, int W, int MB, int GS, bool dx, bool swi) {
   const size_t red = (size_t)2 * W * 16 * MB * 4 + (swi ? (size_t)MB * 16 * 4 : 0);
   if (dx) return red;
-  return (size_t)a.M * a.K * 2 + 64 + (size_t)(a.K / GS) * MB * 4 + red;
+  return (size_t)a.M * xrow_bytes((int)a.K) + 64 + (size_t)(a.K / GS) * MB * 4 + red;
 }
 
 // Blocks per CU: as many as LDS and registers keep resident at once (up to
@@ -1158,7 +1165,7 @@ hipError_t run_qmvx(const QArgs& a) {
   if (W > 16) W = 16;
   if (W < 1) W = 1;
   k.S = (nseg + W - 1) / W;
-  const size_t lds = (size_t)(a.M + 1) * kc * 2 + (size_t)(kc / GS) * RPH * 4 +
+  const size_t lds = (size_t)(a.M + 1) * xrow_bytes(kc) + (size_t)(kc / GS) * RPH * 4 +
                      (size_t)W * Z * a.M * 16 * 4;
   dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)(a.batch < 65535 ? a.batch : 65535));
   auto fn = qmvx_kernel<HQ_BITS, XDT, SDT, MB, GS>;
