@@ -19,6 +19,8 @@ Printed JSON line (one, on stdout):
   qmv_shapes    per-projection mean launch time and GB/s (one graph over
                 >= 1 GiB of distinct copies of that projection)
   qmv_batch     the decode step at B = 1, 4, 8
+  mid_rows      16 / 32 / 64 / 127 rows at the gate/up shape (plain product
+                and fused gate/up + SwiGLU), GB/s and fraction of HBM peak
   qmm           configs[2]: M = 2048 prefill GEMMs, TFLOP/s and fraction of
                 the 2.5 PFLOP/s dense bf16 MFMA peak
   moe           configs[4]: sorted gather_qmm (gate, down) at the MoE shapes,
@@ -559,6 +561,48 @@ def bench_batch(model, args, step, dev):
     return qb
 
 
+def bench_mid_rows(model, dev, steps):
+    """16 to 127 rows of x (a batch engine with that many active requests, or
+    a short prefill chunk) at the Llama-3-8B gate/up shape: the plain product
+    and the fused gate/up + SwiGLU, over the 32 layers' weights (>= 1 GiB of
+    distinct gate + up weights per replay). Bytes are the algorithmic minimum
+    (weights once); the fraction is of the 8 TB/s HBM peak."""
+    import torch
+
+    from higgs_amd import _lib, gen
+
+    lib = _lib.lib()
+    out = {}
+    N, K = INTER, HIDDEN
+    gates = [model.layers[l]["gate"] for l in range(LAYERS)]
+    ups = [model.layers[l]["up"] for l in range(LAYERS)]
+    for M in (16, 32, 64, 127):
+        x = gen.torch_x(7, (M, K), dev)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+        def run(stream, x=x, y=y, M=M):
+            for (w, s, b) in gates + ups:
+                _lib.check(lib.hq_quantized_matmul(y.data_ptr(), x.data_ptr(), w.data_ptr(),
+                                                   s.data_ptr(), b.data_ptr(), M, N, K, 1,
+                                                   GROUP, BITS, 2, 2, stream))
+
+        def run_swi(stream, x=x, y=y, M=M):
+            for (g, u) in zip(gates, ups):
+                _lib.check(lib.hq_quantized_matmul_swiglu(
+                    y.data_ptr(), x.data_ptr(), g[0].data_ptr(), g[1].data_ptr(),
+                    g[2].data_ptr(), u[0].data_ptr(), u[1].data_ptr(), u[2].data_ptr(), M, N,
+                    K, GROUP, BITS, 2, 2, stream))
+        ms = time_graph(run, steps, 1, dev) / (2 * LAYERS)
+        ms2 = time_graph(run_swi, steps, 1, dev) / LAYERS
+        one = qmv_bytes(M, N, K)
+        swi = 2 * qmv_bytes(M, N, K) - 2 * M * N
+        out[str(M)] = {"us": round(ms * 1e3, 2), "GB/s": round(one / (ms * 1e-3) / 1e9, 1),
+                       "frac": round(one / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                       "swiglu_us": round(ms2 * 1e3, 2),
+                       "swiglu_frac": round(swi / (ms2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def bench_fused(model, args, dev):
     import torch
 
@@ -573,7 +617,8 @@ def bench_fused(model, args, dev):
     return r
 
 
-SECTIONS = ("qmv_shapes", "qmv_batch", "qmm", "moe", "configs", "dequant", "decode_fused")
+SECTIONS = ("qmv_shapes", "qmv_batch", "mid_rows", "qmm", "moe", "configs", "dequant",
+            "decode_fused")
 
 
 def sections(model, args, step, dev):
@@ -582,6 +627,7 @@ def sections(model, args, step, dev):
     table = {
         "qmv_shapes": lambda: bench_shapes(model, args.batch, dev, sub),
         "qmv_batch": lambda: bench_batch(model, args, step, dev),
+        "mid_rows": lambda: bench_mid_rows(model, dev, sub),
         "qmm": lambda: bench_qmm(model, dev, sub),
         "moe": lambda: bench_moe(dev, sub),
         "configs": lambda: bench_configs(dev, sub),
@@ -653,7 +699,7 @@ def main():
 
     log(f"[bench] {_lib.version()} on {torch.cuda.get_device_name(0)}")
     if args.only:
-        needs_model = {"qmv_shapes", "qmv_batch", "qmm", "decode_fused"}
+        needs_model = {"qmv_shapes", "qmv_batch", "mid_rows", "qmm", "decode_fused"}
         model = Model(dev) if needs_model & set(args.only.split(",")) else None
         out = {}
         for name, fn in sections(model, args, None, dev):

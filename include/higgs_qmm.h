@@ -229,9 +229,9 @@ int hq_embedding_dequantize(void* out, const uint32_t* w, const void* scales,
  * Rounding: gate and up are each rounded to x_dtype (as the reference
  * materialises them), swiglu is evaluated in float32 and rounded once.
  * Supported: x_dtype == s_dtype in {float16, bfloat16}, and either
- * M <= 127 with K a multiple of 1024, or M >= 128 with K a multiple of 64.
- * Other shapes return HQ_ERR_UNSUPPORTED; callers then use
- * hq_quantized_matmul for both halves and hq_swiglu.
+ * M <= 11 with K a multiple of 1024 (and M <= 4 when group_size == 32), or
+ * M >= 12 with K a multiple of 64. Other shapes return HQ_ERR_UNSUPPORTED;
+ * callers then use hq_quantized_matmul for both halves and hq_swiglu.
  */
 int hq_quantized_matmul_swiglu(void* h, const void* x, const uint32_t* w_gate,
                                const void* s_gate, const void* b_gate,

@@ -43,7 +43,7 @@ def _dense_case(seed, M, N, K, bits, g, dt):
     return x, w, s, b
 
 
-@pytest.mark.parametrize("M", [1, 2, 5, 8, 20, 256])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 11, 12, 20, 33, 127, 256])
 @pytest.mark.parametrize("bits,g", [(4, 64), (3, 32), (8, 128)])
 def test_dense_hidden_fused_matches_oracle(dev, M, bits, g):
     N, K, dt = 200, 1024, O.BF16

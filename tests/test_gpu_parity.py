@@ -377,6 +377,17 @@ def test_few_rows_streaming(dev, M, dt, bits, g, N, K):
     _qmm_check(dev, M, N, K, bits, g, dt, dt, seed=N + K + bits * 7 + g + M)
 
 
+# --- 9..127 rows (batched decode of many requests, short prefill chunks) ----
+
+@pytest.mark.parametrize("M", [9, 16, 33, 100, 127])
+@pytest.mark.parametrize("bits,g", [(4, 64), (3, 32), (8, 128), (2, 64)])
+def test_qmm_mid_rows_on_the_gemm(dev, M, bits, g):
+    """Between the GEMV kernels' 8 rows and a full 128-row tile the product
+    runs on the large-tile GEMM (ragged rows, split K); sampled rows vs the
+    oracle."""
+    _sampled_rows_check(dev, M, 1000, 2048, bits, g, seed=M * 13 + bits + g, n_rows=64)
+
+
 # --- prefill GEMM with K split inside the block (few output tiles) -----------
 
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 4000, 1536), (512, 8000, 1024),
