@@ -95,9 +95,17 @@ __device__ __forceinline__ void dma4(const void* g, void* lds_wave) {
 constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
 
 constexpr int kMR = 64;  // x rows per block pass (four 16-row MFMA tiles)
+// Row stride (floats) of the group sums in LDS for GQ groups per lane group:
+// the fp32 MFMA's A read of lane group q starts q * GQ rows down, and a stride
+// with GQ * stride = 16 (mod 64) puts the four lane groups on disjoint banks.
+constexpr int xsum_stride(int gq) {
+  int s = kMR;
+  while ((gq * s) % 64 != 16) s++;
+  return s;
+}
 // LDS of one block: group sums, the out-of-range flags, x rows of K + 8 elements.
 template <int GS, int K>
-constexpr int gx_lds_bytes() { return (K / GS) * kMR * 4 + kMR * 4 + kMR * (K + 8) * 2; }
+constexpr int gx_lds_bytes() { return (K / GS) * xsum_stride(K / GS / 4) * 4 + kMR * 4 + kMR * (K + 8) * 2; }
 
 template <int XDT, int GS, int KC>
 __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
@@ -109,16 +117,13 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
                                     // 16 lanes reading 16 B of 16 rows hit 16 bank groups)
   constexpr int MR = kMR;
   constexpr int RPW = MR / 8;       // x rows each of the 8 waves stages
-  // An item is one K part (CP chunks of 256) of one 16-row W tile: at most 4
-  // chunks (32 words per lane), so two items in flight fit the registers.
-  constexpr int CP = KC % 4 == 0 ? 4 : (KC % 3 == 0 ? 3 : KC);
-  constexpr int KP = KC / CP;       // parts per tile
-  constexpr int GP = G / KP;        // groups per part
-  constexpr int WPP = GP / 2;       // scale words per part
-  constexpr int SW = (WPP + 3) / 4; // scale words each lane group q holds
-  constexpr int NWL = CP * NGC;     // weight load instructions per item
+  // An item is one 16-row W tile over the whole K (at most 4 chunks of 256:
+  // 32 words per lane, so two items in flight fit the registers).
+  constexpr int GQ = G / 4;         // scale groups each lane group q owns: q, q + 4, ...
+  constexpr int NWL = KC * NGC;     // weight load instructions per item
   static_assert(WPG == 2 || WPG == 4, "group size 64 or 128");
-  static_assert(GP % 2 == 0 && KC % CP == 0, "whole scale words per part");
+  static_assert(KC <= 4 && G % 4 == 0, "K <= 1024, whole fp32-MFMA steps of groups");
+  constexpr int XSS = xsum_stride(GQ);
   static_assert(gx_lds_bytes<GS, KK>() <= 160 * 1024, "x rows fit the LDS");
   using T = SMma<XDT>;
   using frag = typename T::frag;
@@ -127,9 +132,9 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
   // the small arrays first, so every group-sum read folds its offset into
   // the instruction (LDS offsets stop at 64 KB)
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  float* Xs = reinterpret_cast<float*>(smem);                              // [G][MR] group sums
-  int* xbad = reinterpret_cast<int*>(smem + G * MR * 4);                   // [MR]
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + G * MR * 4 + MR * 4);  // [MR][XLD]
+  float* Xs = reinterpret_cast<float*>(smem);                                // [G][XSS] group sums
+  int* xbad = reinterpret_cast<int*>(smem + G * XSS * 4);                    // [MR]
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + G * XSS * 4 + MR * 4);  // [MR][XLD]
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nl = lane & 15, q = lane >> 4;
@@ -152,50 +157,47 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
     return;
   }
 
-  // this wave's tiles: tb + wv + 8j; item i = j * KP + part
-  const int ntw = max(0, (te - tb - wv + 7) / 8);
-  const int NI = ntw * KP;
+  // this wave's tiles: tb + wv + 8j; item i = tile j
+  const int NI = max(0, (te - tb - wv + 7) / 8);
   const int64_t P = KK / 8;  // words per W row
 
+  // Lane group q owns the scales and biases of groups [q * GQ, q * GQ + GQ):
+  // packed in words when GQ is even, one 16-bit value per register otherwise.
+  constexpr bool PK = GQ % 2 == 0;
+  constexpr int SBW = PK ? GQ / 2 : GQ;
   struct Buf {
-    uint32_t wd[CP][8];
-    uint32_t sv[SW], bv[SW];  // scale / bias words q*SW .. of the part
+    uint32_t wd[KC][8];
+    uint32_t sv[SBW], bv[SBW];
   };
-  // row of W and part of item i (clamped to the last item: loads past the end
-  // reload it and are never computed)
-  auto item_at = [&](int i, int& part) __attribute__((always_inline)) -> int64_t {
-    const int ii = min(i, max(NI - 1, 0));
-    part = ii % KP;
-    const int t = min(tb + wv + 8 * (ii / KP), te - 1);
+  // W row of item i (clamped to the last item: loads past the end reload it
+  // and are never computed)
+  auto item_row = [&](int i) __attribute__((always_inline)) -> int64_t {
+    const int t = min(tb + wv + 8 * min(i, max(NI - 1, 0)), te - 1);
     return e * N + min(t * 16 + nl, N - 1);
   };
   auto issue_sb = [&](Buf& b, int i) __attribute__((always_inline)) {
-    int part;
-    const int64_t row = item_at(i, part);
-    const uint32_t* sp = reinterpret_cast<const uint32_t*>((const XS*)a.s + row * G) + part * WPP;
-    const uint32_t* bp = reinterpret_cast<const uint32_t*>((const XS*)a.b + row * G) + part * WPP;
-    if constexpr (SW * 4 == WPP && SW == 2) {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(sp + q * 2), u = *reinterpret_cast<const u32x2*>(bp + q * 2);
+    const int64_t row = item_row(i);
+    const XS* sp = (const XS*)a.s + row * G + q * GQ;
+    const XS* bp = (const XS*)a.b + row * G + q * GQ;
+    if constexpr (GQ == 4) {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(sp), u = *reinterpret_cast<const u32x2*>(bp);
       b.sv[0] = v[0]; b.sv[1] = v[1]; b.bv[0] = u[0]; b.bv[1] = u[1];
-    } else if constexpr (SW * 4 == WPP && SW == 4) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(sp + q * 4), u = *reinterpret_cast<const u32x4*>(bp + q * 4);
+    } else if constexpr (GQ == 2) {
+      b.sv[0] = *reinterpret_cast<const uint32_t*>(sp);
+      b.bv[0] = *reinterpret_cast<const uint32_t*>(bp);
+    } else {
 #pragma unroll
-      for (int j = 0; j < 4; j++) { b.sv[j] = v[j]; b.bv[j] = u[j]; }
-    } else {  // words past the part are clamped (never used)
-#pragma unroll
-      for (int j = 0; j < SW; j++) {
-        const int wi = min(q * SW + j, WPP - 1);
-        b.sv[j] = sp[wi];
-        b.bv[j] = bp[wi];
+      for (int t = 0; t < GQ; t++) {
+        b.sv[t] = sp[t];
+        b.bv[t] = bp[t];
       }
     }
   };
   auto issue_w = [&](Buf& b, int i) __attribute__((always_inline)) {
-    int part;
-    const int64_t row = item_at(i, part);
-    const uint32_t* wp = a.w + row * P + part * (CP * 32) + q * WPG;
+    const int64_t row = item_row(i);
+    const uint32_t* wp = a.w + row * P + q * WPG;
 #pragma unroll
-    for (int c = 0; c < CP; c++)
+    for (int c = 0; c < KC; c++)
 #pragma unroll
       for (int g = 0; g < NGC; g++) {
         if constexpr (WPG == 2) {
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
           o[3] = (d[1] >> 16) | (d[3] & 0xffff0000u);
           *reinterpret_cast<u32x4*>(p + pc * 8) = o;
         }
-        Xs[g * MR + row] = sum;
+        Xs[g * XSS + row] = sum;
       }
     }
     // LDS writes done; the weight loads stay in flight
@@ -302,7 +304,6 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
     // items of MT active 16-row tiles, weights double-buffered in registers
     auto run_items = [&](auto mt_c) __attribute__((always_inline)) {
       constexpr int MT = decltype(mt_c)::value;
-      float acc[MT][4];
       auto compute = [&](const Buf& b, int i) __attribute__((always_inline)) {
         // x and its sums do not change across items: without this the
         // compiler hoists every A-fragment read out of the item loop
@@ -311,17 +312,34 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
         // recomputed per item instead of living across the loop
         int qo = q, nlo = nl;
         asm volatile("" : "+v"(qo), "+v"(nlo));
-        const int part = i % KP;
-        if (part == 0) {
+        // this lane's scales s and c = b - OFF * s, groups qo * GQ + t
+        float sf[GQ], cf[GQ];
 #pragma unroll
-          for (int j = 0; j < MT; j++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) acc[j][v] = 0.f;
+        for (int t = 0; t < GQ; t++) {
+          const uint32_t sh = PK ? (b.sv[t / 2] >> (16 * (t & 1))) & 0xffffu : b.sv[t];
+          const uint32_t bh = PK ? (b.bv[t / 2] >> (16 * (t & 1))) & 0xffffu : b.bv[t];
+          sf[t] = DT_<XDT>::to_f32((uint16_t)sh);
+          cf[t] = fmaf(-T::OFF, sf[t], DT_<XDT>::to_f32((uint16_t)bh));
         }
-        const uint16_t* xrow = xs + nlo * XLD + part * (CP * 256) + qo * (GS / 4);
-        const float* xsum = Xs + part * GP * MR + 4 * qo;
+        // the bias term sum_g X[m][g] * c[g][n] on the fp32 matrix cores:
+        // k slot q of step t is group qo * GQ + t, A = X of x row m = nl,
+        // B = c of W row n = nl (the D layout is the bf16 MFMA's)
+        floatx4 acc[MT];
+        const float* xsum = Xs + qo * GQ * XSS + nlo;
 #pragma unroll
-        for (int c = 0; c < CP; c++)
+        for (int j = 0; j < MT; j++) {
+          acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < GQ; t++)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xsum[t * XSS + 16 * j], cf[t], acc[j], 0, 0, 0);
+        }
+        // byte addresses of lane nl of each lane group, for the scale broadcast
+        int src[4];
+#pragma unroll
+        for (int o = 0; o < 4; o++) src[o] = (nlo + 16 * o) * 4;
+        const uint16_t* xrow = xs + nlo * XLD + qo * (GS / 4);
+#pragma unroll
+        for (int c = 0; c < KC; c++)
 #pragma unroll
           for (int g = 0; g < NGC; g++) {
             __builtin_amdgcn_sched_barrier(0);  // one group at a time (bounded live registers)
@@ -342,28 +360,20 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
                 D[j] = T::mma(__builtin_bit_cast(frag, av), __builtin_bit_cast(frag, bw), D[j]);
               }
             }
-            const int gl = c * NGC + g;  // group within the part
-            const int wi = gl / 2, owner = wi / SW, sl = wi % SW;
-            const uint32_t swd = __shfl(b.sv[sl], nlo + 16 * owner, 64);
-            const uint32_t bwd = __shfl(b.bv[sl], nlo + 16 * owner, 64);
-            const float sv = DT_<XDT>::to_f32((uint16_t)((swd >> (16 * (gl & 1))) & 0xffffu));
-            const float bo = fmaf(-T::OFF, sv, DT_<XDT>::to_f32((uint16_t)((bwd >> (16 * (gl & 1))) & 0xffffu)));
+            const int gl = c * NGC + g;
+            const float sv = __int_as_float(__builtin_amdgcn_ds_bpermute(src[gl / GQ], __float_as_int(sf[gl % GQ])));
 #pragma unroll
             for (int j = 0; j < MT; j++) {
-              const floatx4 X = *reinterpret_cast<const floatx4*>(xsum + gl * MR + 16 * j);
 #pragma unroll
-              for (int v = 0; v < 4; v++) {
-                acc[j][v] = fmaf(sv, D[j][v], fmaf(bo, X[v], acc[j][v]));
-                // pin the group's epilogue here: left free, the compiler
-                // sinks every group's FMAs below all the MFMAs and keeps
-                // each group's partial sums live (hundreds of registers)
-                asm volatile("" : "+v"(acc[j][v]));
-              }
+              for (int v = 0; v < 4; v++) acc[j][v] = fmaf(sv, D[j][v], acc[j][v]);
+              // pin the group's epilogue here: left free, the compiler sinks
+              // every group's FMAs below all the MFMAs and keeps each group's
+              // partial sums live (hundreds of registers)
+              asm volatile("" : "+v"(acc[j]));
             }
           }
-        if (part != KP - 1) return;
         // acc[j][v] = y[row 16j + 4q + v][column t*16 + nl]
-        const int t = tb + wv + 8 * (i / KP);
+        const int t = tb + wv + 8 * i;
         const int col = t * 16 + nlo;
         if (col >= N) return;
         XS* yp = yg + (r0 + 4 * qo) * N + col;  // row 4q of the pass
