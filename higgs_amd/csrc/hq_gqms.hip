@@ -352,59 +352,82 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
         // A side: step t of a group takes x elements 8 * wq(t) .. + 7 of the
         // group, wq(t) the word the lane's B register holds at that step
         const uint16_t* xrow = xs + xrow_off(nlo, KK) + (WPG == 4 ? qo * 32 : ((qo & 1) * 4 + (qo >> 1) * 2) * 8);
+        // Software pipeline over the item's G groups: step gg issues the A
+        // reads of group gg + 1 and the scale broadcast of group gg, runs the
+        // MFMAs of group gg and the epilogue of group gg - 1, whose products
+        // are complete by then (LDS and MFMA latency off the critical path).
+        u32x4 A[2][MT][WPG];
+        auto load_a = [&](int gg) __attribute__((always_inline)) {
+          const int c = gg / NGC, g = gg % NGC;
+#pragma unroll
+          for (int j = 0; j < MT; j++)
+#pragma unroll
+            for (int t = 0; t < WPG; t++)
+              A[gg & 1][j][t] = *reinterpret_cast<const u32x4*>(xrow + 16 * j * XLD + c * 256 + g * GS + 8 * t);
+        };
         uint32_t pair[4];  // the regrouped span of the current group pair (group size 64)
+        floatx4 Dp[MT];
+        float svp = 0.f;
+        load_a(0);
 #pragma unroll
-        for (int c = 0; c < KC; c++)
+        for (int gg = 0; gg < G; gg++) {
+          __builtin_amdgcn_sched_barrier(0);  // one group at a time (bounded live registers)
+          const int c = gg / NGC, g = gg % NGC;
+          if (gg + 1 < G) load_a(gg + 1);
+          const float sv = __int_as_float(__builtin_amdgcn_ds_bpermute(src[gg / GQ], __float_as_int(sf[gg % GQ])));
+          uint32_t gw[WPG];
+          if constexpr (WPG == 4) {
 #pragma unroll
-          for (int g = 0; g < NGC; g++) {
-            __builtin_amdgcn_sched_barrier(0);  // one group at a time (bounded live registers)
-            floatx4 D[MT];
-#pragma unroll
-            for (int j = 0; j < MT; j++) D[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-            uint32_t gw[WPG];
-            if constexpr (WPG == 4) {
-#pragma unroll
-              for (int t = 0; t < 4; t++) gw[t] = b.wd[c][4 * g + t];
-            } else {
-              // span h = g / 2 holds words 4q..4q+3: lane groups 0, 1 have
-              // group 2h, lane groups 2, 3 group 2h + 1. Swapping registers
-              // 0 <-> 2 and 1 <-> 3 between the wave halves leaves group 2h
-              // in registers 0, 1 of every lane (words (q&1)*4 + (q>>1)*2 + t)
-              // and group 2h + 1 in registers 2, 3.
-              if ((g & 1) == 0) {
-                const auto s0 = __builtin_amdgcn_permlane32_swap(b.wd[c][2 * g], b.wd[c][2 * g + 2], false, false);
-                const auto s1 = __builtin_amdgcn_permlane32_swap(b.wd[c][2 * g + 1], b.wd[c][2 * g + 3], false, false);
-                pair[0] = s0[0]; pair[1] = s1[0]; pair[2] = s0[1]; pair[3] = s1[1];
-              }
-              gw[0] = pair[2 * (g & 1)];
-              gw[1] = pair[2 * (g & 1) + 1];
+            for (int t = 0; t < 4; t++) gw[t] = b.wd[c][4 * g + t];
+          } else {
+            // span h = g / 2 holds words 4q..4q+3: lane groups 0, 1 have
+            // group 2h, lane groups 2, 3 group 2h + 1. Swapping registers
+            // 0 <-> 2 and 1 <-> 3 between the wave halves leaves group 2h
+            // in registers 0, 1 of every lane (words (q&1)*4 + (q>>1)*2 + t)
+            // and group 2h + 1 in registers 2, 3.
+            if ((g & 1) == 0) {
+              const auto s0 = __builtin_amdgcn_permlane32_swap(b.wd[c][2 * g], b.wd[c][2 * g + 2], false, false);
+              const auto s1 = __builtin_amdgcn_permlane32_swap(b.wd[c][2 * g + 1], b.wd[c][2 * g + 3], false, false);
+              pair[0] = s0[0]; pair[1] = s1[0]; pair[2] = s0[1]; pair[3] = s1[1];
             }
+            gw[0] = pair[2 * (g & 1)];
+            gw[1] = pair[2 * (g & 1) + 1];
+          }
+          floatx4 D[MT];
 #pragma unroll
-            for (int t = 0; t < WPG; t++) {
-              const uint32_t w = gw[t];
-              u32x4 bw;
-              bw[0] = (w & mask_s) | off_v;
-              bw[1] = ((w >> 4) & mask_s) | off_v;
-              bw[2] = ((w >> 8) & mask_s) | off_v;
-              bw[3] = ((w >> 12) & mask_s) | off_v;
+          for (int j = 0; j < MT; j++) D[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-              for (int j = 0; j < MT; j++) {
-                const u32x4 av = *reinterpret_cast<const u32x4*>(xrow + 16 * j * XLD + c * 256 + g * GS + 8 * t);
-                D[j] = T::mma(__builtin_bit_cast(frag, av), __builtin_bit_cast(frag, bw), D[j]);
-              }
-            }
-            const int gl = c * NGC + g;
-            const float sv = __int_as_float(__builtin_amdgcn_ds_bpermute(src[gl / GQ], __float_as_int(sf[gl % GQ])));
+          for (int t = 0; t < WPG; t++) {
+            const uint32_t w = gw[t];
+            u32x4 bw;
+            bw[0] = (w & mask_s) | off_v;
+            bw[1] = ((w >> 4) & mask_s) | off_v;
+            bw[2] = ((w >> 8) & mask_s) | off_v;
+            bw[3] = ((w >> 12) & mask_s) | off_v;
+#pragma unroll
+            for (int j = 0; j < MT; j++)
+              D[j] = T::mma(__builtin_bit_cast(frag, A[gg & 1][j][t]), __builtin_bit_cast(frag, bw), D[j]);
+          }
+          if (gg > 0) {
 #pragma unroll
             for (int j = 0; j < MT; j++) {
 #pragma unroll
-              for (int v = 0; v < 4; v++) acc[j][v] = fmaf(sv, D[j][v], acc[j][v]);
-              // pin the group's epilogue here: left free, the compiler sinks
-              // every group's FMAs below all the MFMAs and keeps each group's
-              // partial sums live (hundreds of registers)
+              for (int v = 0; v < 4; v++) acc[j][v] = fmaf(svp, Dp[j][v], acc[j][v]);
+              // pin the epilogue to its step: left free, the compiler sinks
+              // every group's FMAs to the end and keeps each group's partial
+              // sums live (hundreds of registers)
               asm volatile("" : "+v"(acc[j]));
             }
           }
+#pragma unroll
+          for (int j = 0; j < MT; j++) Dp[j] = D[j];
+          svp = sv;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < MT; j++)
+#pragma unroll
+          for (int v = 0; v < 4; v++) acc[j][v] = fmaf(svp, Dp[j][v], acc[j][v]);
         // acc[j][v] = y[row 16j + 4q + v][column t*16 + nl]
         const int t = tb + wv + 8 * i;
         const int col = t * 16 + nlo;
