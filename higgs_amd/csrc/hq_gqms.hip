@@ -1,7 +1,8 @@
 // hq_gqms.hip -- sorted-expert grouped quantized matmul, streaming form, for
 // 4-bit weights: gather_qmm with sorted rhs indices (the MoE expert GEMM of
-// crates/higgs-models/src/qwen3_next.rs:1764-1799, FFI at 509-578) when each
-// expert has few routed rows and K <= 1024, as in the MoE down projection.
+// crates/higgs-models/src/qwen3_next.rs:1764-1799, FFI at 509-578) and its
+// fused gate/up + SwiGLU form (qwen3_next.rs:1764-1787), when each expert has
+// few routed rows and K <= 2048, as in the MoE projections.
 //
 // y[r, n] = sum_k x[xi(r), k] * (s[e, n, g] * q[e, n, k] + b[e, n, g]),
 // e = rhs[r / M] (non-decreasing), g = k / group_size.
@@ -14,21 +15,20 @@
 //   acc += s * D_g + (b - OFF * s) * X_g,   X_g = sum of x over the group.
 //
 // Layout of one v_mfma_f32_16x16x32 step: B = 16 W rows (lane n = lane % 16)
-// x 32 k, A = 16 x rows, D[m, n]. For every MFMA step to stay inside one
-// scale group, lane group q = lane / 16 loads words [q*WPG, q*WPG + WPG) of
-// each group (WPG = group_size / 32 words), and step t of the group uses word
-// t: elements g*GS + q*GS/4 + 8t + (0..7), the unpack giving the pairs
-// (j, j + 4); x sits in LDS in that pair order (0,4,1,5,2,6,3,7) per
-// 8-element block.
+// x 32 k, A = 16 x rows, D[m, n]. Every MFMA step stays inside one scale
+// group: at group size 128 lane group q = lane / 16 holds words [4q, 4q + 4)
+// of the group, at 64 the words of a group pair are regrouped across the wave
+// halves (see the compute step); x sits in LDS in the unpack's pair order
+// (0,4,1,5,2,6,3,7) per 8-element block.
 //
-// Block (tile range, e): 8 waves. The block finds the run of rows routed to
-// e by a wave-wide search over the sorted indices (unused experts cost no
-// weight traffic), loads up to 64 of those rows of x for the whole K straight
-// into LDS (global_load_lds_dwordx4), computes the group sums (v_dot2 against
-// ones) and reorders x to the pair order in place, then each wave streams its
-// 16-row W tiles through a register double buffer while it multiplies. The
-// block row e == w_batch fills rows of out-of-range expert indices with NaN,
-// and rows whose x index is out of range are NaN too.
+// Block (tile range, e, z): 8 waves. The block finds the run of rows routed
+// to e by a wave-wide search over the sorted indices (unused experts cost no
+// weight traffic), loads up to 64 (32) of those rows of x for the whole K
+// straight into LDS (global_load_lds_dwordx4), computes the group sums (v_dot2
+// against ones) and reorders x to the pair order in place, then each wave
+// streams its 16-row W tiles through a register double buffer while it
+// multiplies. The block row e == w_batch fills rows of out-of-range expert
+// indices with NaN, and rows whose x index is out of range are NaN too.
 #include <atomic>
 #include <type_traits>
 
@@ -57,6 +57,9 @@ struct GSKern {
   uint32_t nib_mask, off_pair;  // 0x000F000F and the (OFF, OFF) pair, kept out of literals
   int ntiles;                   // 16-column output tiles: ceil(N / 16)
   int ns;                       // blocks splitting the tiles (grid.x)
+  const uint32_t* w2;           // fused SwiGLU: the up projection (w, s, b are the gate)
+  const void* s2;
+  const void* b2;
 };
 
 template <int XDT> struct SMma;
@@ -118,27 +121,44 @@ constexpr int xrow_elems(int k) { return k + 128; }
 __device__ __forceinline__ int xrow_off(int r, int k) {
   return r * xrow_elems(k) + 8 * (int)((kRowSlot >> (4 * (r & 15))) & 15);
 }
+// Shape of one instantiation: KC chunks of 256 k; an item is one 16-row W
+// tile over CP of them (a K part), so that two items of weights fit the
+// registers; NS weight streams (2: gate and up of the fused SwiGLU); MR x
+// rows per pass: 32 for K = 2048 (x then takes 139 KB of LDS) and for the
+// SwiGLU form (two streams of four 16-row tiles would spill); with 32-row
+// passes the passes of an expert alternate between ZS = 2 blocks.
+template <int KC, bool SWI> struct GSShape {
+  static constexpr int CP = SWI ? 2 : (KC % 4 == 0 ? 4 : KC);
+  static constexpr int KP = KC / CP;
+  static constexpr int NS = SWI ? 2 : 1;
+  static constexpr int MR = KC <= 4 && !SWI ? 64 : 32;
+  static constexpr int ZS = 64 / MR;
+};
 // LDS of one block: group sums, the out-of-range flags, the x rows.
-template <int GS, int K>
-constexpr int gx_lds_bytes() { return (K / GS) * xsum_stride(K / GS / 4) * 4 + kMR * 4 + kMR * xrow_elems(K) * 2; }
+template <int GS, int KC, bool SWI>
+constexpr int gx_lds_bytes() {
+  using SH = GSShape<KC, SWI>;
+  return (KC * 256 / GS) * xsum_stride(SH::CP * (256 / GS) / 4) * 4 + SH::MR * 4 +
+         SH::MR * xrow_elems(KC * 256) * 2;
+}
 
-template <int XDT, int GS, int KC>
+template <int XDT, int GS, int KC, bool SWI>
 __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
+  using SH = GSShape<KC, SWI>;
   constexpr int KK = KC * 256;
   constexpr int G = KK / GS;        // scale groups per W row
   constexpr int NGC = 256 / GS;     // groups per 256-element chunk
   constexpr int WPG = GS / 32;      // words per lane per group (2 or 4)
   constexpr int XLD = xrow_elems(KK);  // LDS row stride of x in elements
-  constexpr int MR = kMR;
+  constexpr int CP = SH::CP, KP = SH::KP, NS = SH::NS, MR = SH::MR, ZS = SH::ZS;
   constexpr int RPW = MR / 8;       // x rows each of the 8 waves stages
-  // An item is one 16-row W tile over the whole K (at most 4 chunks of 256:
-  // 32 words per lane, so two items in flight fit the registers).
-  constexpr int GQ = G / 4;         // scale groups each lane group q owns: q, q + 4, ...
-  constexpr int NWL = KC * 2;       // weight load instructions per item (16 bytes per lane)
+  constexpr int GPP = CP * NGC;     // scale groups per item part
+  constexpr int GQ = GPP / 4;       // groups of a part each lane group owns
+  constexpr int NWL = NS * CP * 2;  // weight load instructions per item (16 bytes per lane)
   static_assert(WPG == 2 || WPG == 4, "group size 64 or 128");
-  static_assert(KC <= 4 && G % 4 == 0, "K <= 1024, whole fp32-MFMA steps of groups");
+  static_assert(KC % CP == 0 && GPP % 4 == 0, "whole parts, whole fp32-MFMA steps of groups");
   constexpr int XSS = xsum_stride(GQ);
-  static_assert(gx_lds_bytes<GS, KK>() <= 160 * 1024, "x rows fit the LDS");
+  static_assert(gx_lds_bytes<GS, KC, SWI>() <= 160 * 1024, "x rows fit the LDS");
   using T = SMma<XDT>;
   using frag = typename T::frag;
   using XS = st_t<XDT>;
@@ -154,6 +174,7 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
   const int nl = lane & 15, q = lane >> 4;
   const int N = a.N, M = a.M;
   const int64_t e = blockIdx.y;
+  const int z = (int)blockIdx.z;
   const int tpb = (a.ntiles + a.ns - 1) / a.ns;
   const int tb = blockIdx.x * tpb, te = min(a.ntiles, tb + tpb);
   if (tb >= te) return;
@@ -161,67 +182,79 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
   const int64_t s0 = wave_lower_bound(a.rhs, a.batch, (uint32_t)e);
   const int64_t s1 = expert_ok ? wave_lower_bound(a.rhs, a.batch, (uint32_t)(e + 1)) : a.batch;
   const int64_t r_begin = s0 * M, r_end = s1 * M;  // flattened (element, m) rows
-  if (r_begin >= r_end) return;  // block-uniform
+  if (r_begin + (int64_t)z * MR >= r_end) return;  // block-uniform
   XS* yg = (XS*)a.y;
   constexpr uint16_t kNaN = XDT == DT_BF16 ? 0x7fc0u : 0x7e00u;
   if (!expert_ok) {
+    if (z != 0) return;
     const int c0 = tb * 16, c1 = min(te * 16, N);
     for (int64_t r = r_begin; r < r_end; r++)
       for (int n = c0 + tid; n < c1; n += 512) yg[r * N + n] = kNaN;
     return;
   }
 
-  // this wave's tiles: tb + wv + 8j; item i = tile j
-  const int NI = max(0, (te - tb - wv + 7) / 8);
+  // this wave's tiles: tb + wv + 8j; item i = part i % KP of tile j = i / KP
+  const int NI = max(0, (te - tb - wv + 7) / 8) * KP;
   const int64_t P = KK / 8;  // words per W row
 
-  // Lane group q owns the scales and biases of groups [q * GQ, q * GQ + GQ):
-  // packed in words when GQ is even, one 16-bit value per register otherwise.
+  // Lane group q owns the scales and biases of groups [q * GQ, q * GQ + GQ)
+  // of a part: packed in words when GQ is even, one 16-bit value per register
+  // otherwise.
   constexpr bool PK = GQ % 2 == 0;
   constexpr int SBW = PK ? GQ / 2 : GQ;
   struct Buf {
-    uint32_t wd[KC][8];
-    uint32_t sv[SBW], bv[SBW];
+    uint32_t wd[NS][CP][8];
+    uint32_t sv[NS][SBW], bv[NS][SBW];
   };
-  // W row of item i (clamped to the last item: loads past the end reload it
-  // and are never computed)
-  auto item_row = [&](int i) __attribute__((always_inline)) -> int64_t {
-    const int t = min(tb + wv + 8 * min(i, max(NI - 1, 0)), te - 1);
+  // W row and part of item i (clamped to the last item: loads past the end
+  // reload it and are never computed)
+  auto item_at = [&](int i, int& part) __attribute__((always_inline)) -> int64_t {
+    const int ii = min(i, max(NI - 1, 0));
+    part = ii % KP;
+    const int t = min(tb + wv + 8 * (ii / KP), te - 1);
     return e * N + min(t * 16 + nl, N - 1);
   };
   auto issue_sb = [&](Buf& b, int i) __attribute__((always_inline)) {
-    const int64_t row = item_row(i);
-    const XS* sp = (const XS*)a.s + row * G + q * GQ;
-    const XS* bp = (const XS*)a.b + row * G + q * GQ;
-    if constexpr (GQ == 4) {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(sp), u = *reinterpret_cast<const u32x2*>(bp);
-      b.sv[0] = v[0]; b.sv[1] = v[1]; b.bv[0] = u[0]; b.bv[1] = u[1];
-    } else if constexpr (GQ == 2) {
-      b.sv[0] = *reinterpret_cast<const uint32_t*>(sp);
-      b.bv[0] = *reinterpret_cast<const uint32_t*>(bp);
-    } else {
+    int part;
+    const int64_t row = item_at(i, part);
 #pragma unroll
-      for (int t = 0; t < GQ; t++) {
-        b.sv[t] = sp[t];
-        b.bv[t] = bp[t];
+    for (int s = 0; s < NS; s++) {
+      const XS* sp = (const XS*)(s ? a.s2 : a.s) + row * G + part * GPP + q * GQ;
+      const XS* bp = (const XS*)(s ? a.b2 : a.b) + row * G + part * GPP + q * GQ;
+      if constexpr (GQ == 4) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(sp), u = *reinterpret_cast<const u32x2*>(bp);
+        b.sv[s][0] = v[0]; b.sv[s][1] = v[1]; b.bv[s][0] = u[0]; b.bv[s][1] = u[1];
+      } else if constexpr (GQ == 2) {
+        b.sv[s][0] = *reinterpret_cast<const uint32_t*>(sp);
+        b.bv[s][0] = *reinterpret_cast<const uint32_t*>(bp);
+      } else {
+#pragma unroll
+        for (int t = 0; t < GQ; t++) {
+          b.sv[s][t] = sp[t];
+          b.bv[s][t] = bp[t];
+        }
       }
     }
   };
   // 16 bytes per lane: lane group q loads words [4q, 4q + 4) of each
   // 16-word span of the row (64 contiguous bytes per row per instruction).
-  // At group size 128 a span is one group; at 64 it is two, and
-  // take_pairs() below regroups the words across the wave halves.
+  // At group size 128 a span is one group; at 64 it is two, and the compute
+  // step regroups the words across the wave halves.
   auto issue_w = [&](Buf& b, int i) __attribute__((always_inline)) {
-    const int64_t row = item_row(i);
-    const uint32_t* wp = a.w + row * P + q * 4;
+    int part;
+    const int64_t row = item_at(i, part);
 #pragma unroll
-    for (int c = 0; c < KC; c++)
+    for (int s = 0; s < NS; s++) {
+      const uint32_t* wp = (s ? a.w2 : a.w) + row * P + part * (CP * 32) + q * 4;
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(wp + c * 32 + h * 16);
+      for (int c = 0; c < CP; c++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) b.wd[c][4 * h + t] = v[t];
-      }
+        for (int h = 0; h < 2; h++) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(wp + c * 32 + h * 16);
+#pragma unroll
+          for (int t = 0; t < 4; t++) b.wd[s][c][4 * h + t] = v[t];
+        }
+    }
   };
 
   const uint32_t mask_s = a.nib_mask;
@@ -229,7 +262,7 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
   asm("v_mov_b32 %0, %1" : "=v"(off_v) : "s"(a.off_pair));
 
   Buf ba, bb;
-  for (int64_t r0 = r_begin; r0 < r_end; r0 += MR) {
+  for (int64_t r0 = r_begin + (int64_t)z * MR; r0 < r_end; r0 += (int64_t)ZS * MR) {
     const int nrows = (int)min((int64_t)MR, r_end - r0);
     // x row offsets of this wave's rows (token gather through lhs)
     int64_t xoff[RPW];
@@ -313,9 +346,11 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
-    // items of MT active 16-row tiles, weights double-buffered in registers
+    // items of MT active 16-row tiles, weights double-buffered in registers;
+    // the accumulators carry over the KP parts of a tile
     auto run_items = [&](auto mt_c) __attribute__((always_inline)) {
       constexpr int MT = decltype(mt_c)::value;
+      floatx4 acc[NS][MT];
       auto compute = [&](const Buf& b, int i) __attribute__((always_inline)) {
         // x and its sums do not change across items: without this the
         // compiler hoists every A-fragment read out of the item loop
@@ -324,38 +359,50 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
         // recomputed per item instead of living across the loop
         int qo = q, nlo = nl;
         asm volatile("" : "+v"(qo), "+v"(nlo));
-        // this lane's scales s and c = b - OFF * s, groups qo * GQ + t
-        float sf[GQ], cf[GQ];
+        const int part = i % KP;
+        if (part == 0) {
 #pragma unroll
-        for (int t = 0; t < GQ; t++) {
-          const uint32_t sh = PK ? (b.sv[t / 2] >> (16 * (t & 1))) & 0xffffu : b.sv[t];
-          const uint32_t bh = PK ? (b.bv[t / 2] >> (16 * (t & 1))) & 0xffffu : b.bv[t];
-          sf[t] = DT_<XDT>::to_f32((uint16_t)sh);
-          cf[t] = fmaf(-T::OFF, sf[t], DT_<XDT>::to_f32((uint16_t)bh));
+          for (int s = 0; s < NS; s++)
+#pragma unroll
+            for (int j = 0; j < MT; j++) acc[s][j] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
+        // this lane's scales s and c = b - OFF * s, groups qo * GQ + t of the part
+        float sf[NS][GQ], cf[NS][GQ];
+#pragma unroll
+        for (int s = 0; s < NS; s++)
+#pragma unroll
+          for (int t = 0; t < GQ; t++) {
+            const uint32_t sh = PK ? (b.sv[s][t / 2] >> (16 * (t & 1))) & 0xffffu : b.sv[s][t];
+            const uint32_t bh = PK ? (b.bv[s][t / 2] >> (16 * (t & 1))) & 0xffffu : b.bv[s][t];
+            sf[s][t] = DT_<XDT>::to_f32((uint16_t)sh);
+            cf[s][t] = fmaf(-T::OFF, sf[s][t], DT_<XDT>::to_f32((uint16_t)bh));
+          }
         // the bias term sum_g X[m][g] * c[g][n] on the fp32 matrix cores:
-        // k slot q of step t is group qo * GQ + t, A = X of x row m = nl,
-        // B = c of W row n = nl (the D layout is the bf16 MFMA's)
-        floatx4 acc[MT];
-        const float* xsum = Xs + qo * GQ * XSS + nlo;
+        // k slot q of step t is group qo * GQ + t of the part, A = X of x row
+        // m = nl, B = c of W row n = nl (the D layout is the bf16 MFMA's)
+        const float* xsum = Xs + (part * GPP + qo * GQ) * XSS + nlo;
 #pragma unroll
-        for (int j = 0; j < MT; j++) {
-          acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < MT; j++)
 #pragma unroll
-          for (int t = 0; t < GQ; t++)
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xsum[t * XSS + 16 * j], cf[t], acc[j], 0, 0, 0);
-        }
+          for (int t = 0; t < GQ; t++) {
+            const float xa = xsum[t * XSS + 16 * j];
+#pragma unroll
+            for (int s = 0; s < NS; s++)
+              acc[s][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, cf[s][t], acc[s][j], 0, 0, 0);
+          }
         // byte addresses of lane nl of each lane group, for the scale broadcast
         int src[4];
 #pragma unroll
         for (int o = 0; o < 4; o++) src[o] = (nlo + 16 * o) * 4;
         // A side: step t of a group takes x elements 8 * wq(t) .. + 7 of the
         // group, wq(t) the word the lane's B register holds at that step
-        const uint16_t* xrow = xs + xrow_off(nlo, KK) + (WPG == 4 ? qo * 32 : ((qo & 1) * 4 + (qo >> 1) * 2) * 8);
-        // Software pipeline over the item's G groups: step gg issues the A
+        const uint16_t* xrow = xs + xrow_off(nlo, KK) + part * (CP * 256) +
+                               (WPG == 4 ? qo * 32 : ((qo & 1) * 4 + (qo >> 1) * 2) * 8);
+        // Software pipeline over the part's GPP groups: step gg issues the A
         // reads of group gg + 1 and the scale broadcast of group gg, runs the
         // MFMAs of group gg and the epilogue of group gg - 1, whose products
         // are complete by then (LDS and MFMA latency off the critical path).
+        // Both weight streams use the same A fragments.
         u32x4 A[2][MT][WPG];
         auto load_a = [&](int gg) __attribute__((always_inline)) {
           const int c = gg / NGC, g = gg % NGC;
@@ -365,71 +412,85 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
             for (int t = 0; t < WPG; t++)
               A[gg & 1][j][t] = *reinterpret_cast<const u32x4*>(xrow + 16 * j * XLD + c * 256 + g * GS + 8 * t);
         };
-        uint32_t pair[4];  // the regrouped span of the current group pair (group size 64)
-        floatx4 Dp[MT];
-        float svp = 0.f;
+        uint32_t pair[NS][4];  // the regrouped span of the current group pair (group size 64)
+        floatx4 Dp[NS][MT];
+        float svp[NS];
         load_a(0);
 #pragma unroll
-        for (int gg = 0; gg < G; gg++) {
+        for (int gg = 0; gg < GPP; gg++) {
           __builtin_amdgcn_sched_barrier(0);  // one group at a time (bounded live registers)
           const int c = gg / NGC, g = gg % NGC;
-          if (gg + 1 < G) load_a(gg + 1);
-          const float sv = __int_as_float(__builtin_amdgcn_ds_bpermute(src[gg / GQ], __float_as_int(sf[gg % GQ])));
-          uint32_t gw[WPG];
-          if constexpr (WPG == 4) {
+          if (gg + 1 < GPP) load_a(gg + 1);
+          float sv[NS];
 #pragma unroll
-            for (int t = 0; t < 4; t++) gw[t] = b.wd[c][4 * g + t];
-          } else {
-            // span h = g / 2 holds words 4q..4q+3: lane groups 0, 1 have
-            // group 2h, lane groups 2, 3 group 2h + 1. Swapping registers
-            // 0 <-> 2 and 1 <-> 3 between the wave halves leaves group 2h
-            // in registers 0, 1 of every lane (words (q&1)*4 + (q>>1)*2 + t)
-            // and group 2h + 1 in registers 2, 3.
-            if ((g & 1) == 0) {
-              const auto s0 = __builtin_amdgcn_permlane32_swap(b.wd[c][2 * g], b.wd[c][2 * g + 2], false, false);
-              const auto s1 = __builtin_amdgcn_permlane32_swap(b.wd[c][2 * g + 1], b.wd[c][2 * g + 3], false, false);
-              pair[0] = s0[0]; pair[1] = s1[0]; pair[2] = s0[1]; pair[3] = s1[1];
+          for (int s = 0; s < NS; s++)
+            sv[s] = __int_as_float(__builtin_amdgcn_ds_bpermute(src[gg / GQ], __float_as_int(sf[s][gg % GQ])));
+          floatx4 D[NS][MT];
+#pragma unroll
+          for (int s = 0; s < NS; s++) {
+            uint32_t gw[WPG];
+            if constexpr (WPG == 4) {
+#pragma unroll
+              for (int t = 0; t < 4; t++) gw[t] = b.wd[s][c][4 * g + t];
+            } else {
+              // span h = g / 2 holds words 4q..4q+3: lane groups 0, 1 have
+              // group 2h, lane groups 2, 3 group 2h + 1. Swapping registers
+              // 0 <-> 2 and 1 <-> 3 between the wave halves leaves group 2h
+              // in registers 0, 1 of every lane (words (q&1)*4 + (q>>1)*2 + t)
+              // and group 2h + 1 in registers 2, 3.
+              if ((g & 1) == 0) {
+                const auto s0 = __builtin_amdgcn_permlane32_swap(b.wd[s][c][2 * g], b.wd[s][c][2 * g + 2], false, false);
+                const auto s1 = __builtin_amdgcn_permlane32_swap(b.wd[s][c][2 * g + 1], b.wd[s][c][2 * g + 3], false, false);
+                pair[s][0] = s0[0]; pair[s][1] = s1[0]; pair[s][2] = s0[1]; pair[s][3] = s1[1];
+              }
+              gw[0] = pair[s][2 * (g & 1)];
+              gw[1] = pair[s][2 * (g & 1) + 1];
             }
-            gw[0] = pair[2 * (g & 1)];
-            gw[1] = pair[2 * (g & 1) + 1];
-          }
-          floatx4 D[MT];
 #pragma unroll
-          for (int j = 0; j < MT; j++) D[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < MT; j++) D[s][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int t = 0; t < WPG; t++) {
-            const uint32_t w = gw[t];
-            u32x4 bw;
-            bw[0] = (w & mask_s) | off_v;
-            bw[1] = ((w >> 4) & mask_s) | off_v;
-            bw[2] = ((w >> 8) & mask_s) | off_v;
-            bw[3] = ((w >> 12) & mask_s) | off_v;
+            for (int t = 0; t < WPG; t++) {
+              const uint32_t w = gw[t];
+              u32x4 bw;
+              bw[0] = (w & mask_s) | off_v;
+              bw[1] = ((w >> 4) & mask_s) | off_v;
+              bw[2] = ((w >> 8) & mask_s) | off_v;
+              bw[3] = ((w >> 12) & mask_s) | off_v;
 #pragma unroll
-            for (int j = 0; j < MT; j++)
-              D[j] = T::mma(__builtin_bit_cast(frag, A[gg & 1][j][t]), __builtin_bit_cast(frag, bw), D[j]);
+              for (int j = 0; j < MT; j++)
+                D[s][j] = T::mma(__builtin_bit_cast(frag, A[gg & 1][j][t]), __builtin_bit_cast(frag, bw), D[s][j]);
+            }
           }
           if (gg > 0) {
 #pragma unroll
-            for (int j = 0; j < MT; j++) {
+            for (int s = 0; s < NS; s++)
 #pragma unroll
-              for (int v = 0; v < 4; v++) acc[j][v] = fmaf(svp, Dp[j][v], acc[j][v]);
-              // pin the epilogue to its step: left free, the compiler sinks
-              // every group's FMAs to the end and keeps each group's partial
-              // sums live (hundreds of registers)
-              asm volatile("" : "+v"(acc[j]));
-            }
+              for (int j = 0; j < MT; j++) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[s][j][v] = fmaf(svp[s], Dp[s][j][v], acc[s][j][v]);
+                // pin the epilogue to its step: left free, the compiler sinks
+                // every group's FMAs to the end and keeps each group's partial
+                // sums live (hundreds of registers)
+                asm volatile("" : "+v"(acc[s][j]));
+              }
           }
 #pragma unroll
-          for (int j = 0; j < MT; j++) Dp[j] = D[j];
-          svp = sv;
+          for (int s = 0; s < NS; s++) {
+#pragma unroll
+            for (int j = 0; j < MT; j++) Dp[s][j] = D[s][j];
+            svp[s] = sv[s];
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < MT; j++)
+        for (int s = 0; s < NS; s++)
 #pragma unroll
-          for (int v = 0; v < 4; v++) acc[j][v] = fmaf(svp, Dp[j][v], acc[j][v]);
-        // acc[j][v] = y[row 16j + 4q + v][column t*16 + nl]
-        const int t = tb + wv + 8 * i;
+          for (int j = 0; j < MT; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[s][j][v] = fmaf(svp[s], Dp[s][j][v], acc[s][j][v]);
+        if (part != KP - 1) return;
+        // acc[s][j][v] = y[row 16j + 4q + v][column t*16 + nl]
+        const int t = tb + wv + 8 * (i / KP);
         const int col = t * 16 + nlo;
         if (col >= N) return;
         XS* yp = yg + (r0 + 4 * qo) * N + col;  // row 4q of the pass
@@ -439,7 +500,11 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
           for (int v = 0; v < 4; v++) {
             const int m = 16 * j + 4 * qo + v;
             if (m < nrows) {
-              yp[(int64_t)(16 * j + v) * N] = xbad[m] ? kNaN : DT_<XDT>::from_f32(acc[j][v]);
+              // SwiGLU of the two projections, each rounded to the output
+              // type first, as the unfused form materialises them
+              const float y = SWI ? swiglu_f32(DT_<XDT>::round(acc[0][j][v]), DT_<XDT>::round(acc[NS - 1][j][v]))
+                                  : acc[0][j][v];
+              yp[(int64_t)(16 * j + v) * N] = xbad[m] ? kNaN : DT_<XDT>::from_f32(y);
             }
           }
       };
@@ -456,43 +521,55 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
       }
     };
     const int mt = (nrows + 15) / 16;
-    if (mt == 1) run_items(std::integral_constant<int, 1>{});
-    else if (mt == 2) run_items(std::integral_constant<int, 2>{});
-    else if (mt == 3) run_items(std::integral_constant<int, 3>{});
-    else run_items(std::integral_constant<int, 4>{});
+    if constexpr (MR == 32) {
+      if (mt == 1) run_items(std::integral_constant<int, 1>{});
+      else run_items(std::integral_constant<int, 2>{});
+    } else {
+      if (mt == 1) run_items(std::integral_constant<int, 1>{});
+      else if (mt == 2) run_items(std::integral_constant<int, 2>{});
+      else if (mt == 3) run_items(std::integral_constant<int, 3>{});
+      else run_items(std::integral_constant<int, 4>{});
+    }
     __syncthreads();  // x, its sums and xbad are rewritten by the next pass
   }
 }
 
-template <int XDT, int GS, int KC>
+template <int XDT, int GS, int KC, bool SWI>
 hipError_t run_gqms(const QArgs& a) {
-  constexpr int lds = gx_lds_bytes<GS, KC * 256>();
+  constexpr int lds = gx_lds_bytes<GS, KC, SWI>();
   GSKern k;
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b; k.lhs = a.lhs; k.rhs = a.rhs;
+  k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
   k.batch = a.batch; k.x_rep = a.x_rep; k.x_batch = a.x_batch; k.w_batch = a.w_batch;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
   k.nib_mask = 0x000F000Fu;
   k.off_pair = SMma<XDT>::OFFB;
   k.ntiles = (int)((a.N + 15) / 16);
   k.ns = (k.ntiles + 63) / 64;  // up to 64 weight tiles (16 rows x K) per block
-  auto fn = gqms_kernel<XDT, GS, KC>;
+  auto fn = gqms_kernel<XDT, GS, KC, SWI>;
   static std::atomic<uint64_t> raised{0};
   hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), lds, raised);
   if (e != hipSuccess) return e;
-  dim3 grid((unsigned)k.ns, (unsigned)(a.w_batch + 1));
+  dim3 grid((unsigned)k.ns, (unsigned)(a.w_batch + 1), (unsigned)GSShape<KC, SWI>::ZS);
   hipLaunchKernelGGL(fn, grid, dim3(512), lds, a.stream, k);
   return hipGetLastError();
 }
 
-template <int XDT, int GS>
+template <int XDT, int GS, bool SWI>
 hipError_t run_gqms_k(const QArgs& a) {
   switch (a.K / 256) {
-    case 2: return run_gqms<XDT, GS, 2>(a);
-    case 3: if constexpr (GS == 64) return run_gqms<XDT, GS, 3>(a); else break;
-    case 4: return run_gqms<XDT, GS, 4>(a);
+    case 2: return run_gqms<XDT, GS, 2, SWI>(a);
+    case 3: if constexpr (GS == 64 && !SWI) return run_gqms<XDT, GS, 3, SWI>(a); else break;
+    case 4: return run_gqms<XDT, GS, 4, SWI>(a);
+    case 8: return run_gqms<XDT, GS, 8, SWI>(a);
     default: break;
   }
   return hipErrorNotSupported;
+}
+
+template <int XDT, bool SWI>
+hipError_t run_gqms_g(const QArgs& a) {
+  return a.group_size == 64 ? run_gqms_k<XDT, 64, SWI>(a) : run_gqms_k<XDT, 128, SWI>(a);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -504,28 +581,25 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // The streaming grouped kernel, or hipErrorNotSupported for what it does not
 // take: other bit widths, group size 32, mixed or fp32 dtypes, K not one of
-// 512/768/1024 (768 only at group size 64), the fused SwiGLU, scales or
-// biases not 16-byte aligned, more than 64 rows per expert on average (the
+// 512/768/1024/2048 (768 only at group size 64 and unfused), scales or biases
+// not 16-byte aligned, more than 64 rows per expert on average (the
 // LDS-dequant GEMM amortises its dequantization there).
 hipError_t HQ_CAT(launch_gqms_t_b, HQ_BITS)(const QArgs& a) {
   if constexpr (HQ_BITS != 4) {
     (void)a;
     return hipErrorNotSupported;
   } else {
-    // Measured at configs[4] (4096 rows, 128 experts): K = 768 66 us against
-    // the LDS-dequant kernel's 73. With K = 2048 (then only 32 x rows fit the
-    // LDS, and experts of 33-64 rows take two passes) it measured 84 against
-    // 76 us, and with the fused SwiGLU 141 against 80: the kernel is
-    // VALU-bound (13.6 VALU instructions per MFMA), so it takes the unfused
-    // single-pass case only.
-    if (a.w2 || a.xdt != a.sdt || a.xdt == DT_F32 || !a.rhs || a.w_batch + 1 > 65535)
-      return hipErrorNotSupported;
+    // Measured at configs[4] (4096 rows, 128 experts), same box, against the
+    // LDS-dequant kernel: down (K = 768) 50-54 us vs 69-72, gate (K = 2048)
+    // 50-57 vs 75, the fused gate/up + SwiGLU (K = 2048) 90-94 vs 125-128.
+    if (a.xdt != a.sdt || a.xdt == DT_F32 || !a.rhs || a.w_batch + 1 > 65535) return hipErrorNotSupported;
     if (a.group_size != 64 && a.group_size != 128) return hipErrorNotSupported;
-    if (a.K % 256 != 0 || a.K > 1024 || a.M > ((int64_t)1 << 30)) return hipErrorNotSupported;
+    if (a.K % 256 != 0 || a.K > 2048 || a.M > ((int64_t)1 << 30)) return hipErrorNotSupported;
     if (!aligned16(a.s) || !aligned16(a.b)) return hipErrorNotSupported;
+    if (a.w2 && (!aligned16(a.s2) || !aligned16(a.b2))) return hipErrorNotSupported;
     if (a.batch * a.M > 64 * a.w_batch) return hipErrorNotSupported;  // few rows per expert
-    return a.xdt == DT_BF16 ? (a.group_size == 64 ? run_gqms_k<DT_BF16, 64>(a) : run_gqms_k<DT_BF16, 128>(a))
-                            : (a.group_size == 64 ? run_gqms_k<DT_F16, 64>(a) : run_gqms_k<DT_F16, 128>(a));
+    if (a.w2) return a.xdt == DT_BF16 ? run_gqms_g<DT_BF16, true>(a) : run_gqms_g<DT_F16, true>(a);
+    return a.xdt == DT_BF16 ? run_gqms_g<DT_BF16, false>(a) : run_gqms_g<DT_F16, false>(a);
   }
 }
 

@@ -217,7 +217,7 @@ def test_gather_qmm_swiglu_float32_activations_fall_back(dev):
         assert rel_err(got[r:r + 1], ref) <= 1e-3, r
 
 
-@pytest.mark.parametrize("K", [512, 768, 1024])
+@pytest.mark.parametrize("K", [512, 768, 1024, 2048])
 @pytest.mark.parametrize("dt,g", [(O.BF16, 64), (O.F16, 64), (O.BF16, 128), (O.F16, 128)])
 def test_grouped_kernel_skewed_routing(dev, dt, g, K):
     """4-bit sorted gather at groups 64 and 128 with skewed expert loads --
