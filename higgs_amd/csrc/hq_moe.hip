@@ -143,6 +143,114 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(SortArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// The same stable counting sort for n <= kSortSuper in three phases with
+// three block barriers: wave w owns the contiguous elements [w L, (w+1) L)
+// (L a multiple of 64, keys in registers) and counts them per bucket (LDS
+// atomics); one thread per bucket turns the per-wave counts into per-wave
+// offsets and bucket totals, which a block scan turns into bucket starts;
+// then each wave places its elements in order, 64 at a time, with no further
+// barrier (a wave ranks a key among the equal-bucket lanes before it, and the
+// first lane of each bucket advances the wave's offset for that bucket).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kSortThreads) void moe_sort_small_kernel(SortArgs a) {
+  extern __shared__ int sm[];
+  const int NB = a.E + 1;                  // buckets
+  int* start = sm;                         // [NB] bucket totals, then starts
+  int* cnt = sm + NB;                      // [kSortWaves][NB] per-wave counts, then offsets
+  int* runs = cnt + kSortWaves * NB;       // [kSortThreads] scan of per-thread runs
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int n = (int)a.n;
+  const uint32_t E = (uint32_t)a.E;
+  const int L = (n + 64 * kSortWaves - 1) / (64 * kSortWaves) * 64;  // elements per wave
+  const int SC = L / 64;                                              // <= kSortKeys
+
+  for (int j = tid; j < kSortWaves * NB; j += kSortThreads) cnt[j] = 0;
+  uint32_t key[kSortKeys];  // bucket of element wv L + 64 c + lane, 0xffffffff past n
+#pragma unroll
+  for (int c = 0; c < kSortKeys; c++) {
+    const int i = wv * L + 64 * c + lane;
+    const bool in = c < SC && i < n;
+    const uint32_t k = in ? a.idx[i] : 0u;
+    key[c] = in ? (k < E ? k : E) : 0xffffffffu;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < kSortKeys; c++)
+    if (key[c] != 0xffffffffu) atomicAdd(&cnt[wv * NB + key[c]], 1);
+  __syncthreads();
+  // per bucket: exclusive prefix over the waves (in place) and the total
+  for (int b = tid; b < NB; b += kSortThreads) {
+    int s = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; w++) {
+      const int t = cnt[w * NB + b];
+      cnt[w * NB + b] = s;
+      s += t;
+    }
+    start[b] = s;
+  }
+  __syncthreads();
+  // exclusive scan of the totals: each thread a contiguous run, wave 0 scans
+  // the run sums
+  {
+    const int per = (NB + kSortThreads - 1) / kSortThreads;
+    const int b0 = min(tid * per, NB), b1 = min(b0 + per, NB);
+    int run = 0;
+    for (int b = b0; b < b1; b++) run += start[b];
+    runs[tid] = run;
+    __syncthreads();
+    if (wv == 0) {
+      int v[16], s = 0;
+#pragma unroll
+      for (int j = 0; j < 16; j++) { v[j] = runs[lane * 16 + j]; s += v[j]; }
+      int inc = s;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += t;
+      }
+      int ex = inc - s;
+#pragma unroll
+      for (int j = 0; j < 16; j++) { const int t = v[j]; runs[lane * 16 + j] = ex; ex += t; }
+    }
+    __syncthreads();
+    int off = runs[tid];
+    for (int b = b0; b < b1; b++) { const int t = start[b]; start[b] = off; off += t; }
+  }
+  __syncthreads();
+
+  const int kbits = 32 - __clz(NB);  // bits of a bucket number
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int* woff = cnt + wv * NB;         // this wave's running offsets
+#pragma unroll
+  for (int c = 0; c < kSortKeys; c++) {
+    if (c >= SC) break;              // wave-uniform
+    const int i = wv * L + 64 * c + lane;
+    const bool valid = key[c] != 0xffffffffu;
+    const uint32_t kb = valid ? key[c] : 0u;
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < kbits; bit++) {
+      const bool on = (kb >> bit) & 1u;
+      const uint64_t m = __ballot(on);
+      peers &= on ? m : ~m;
+    }
+    const int rank = __popcll(peers & lt);
+    const int pos = valid ? start[kb] + woff[kb] + rank : 0;
+    if (valid) {
+      if (a.order) a.order[pos] = (uint32_t)i;
+      if (a.inv_order) a.inv_order[i] = (uint32_t)pos;
+      if (a.idx_sorted) a.idx_sorted[pos] = kb < E ? kb : a.idx[i];
+      if (a.token_idx) a.token_idx[pos] = (uint32_t)(i / a.top_k);
+    }
+    // every lane has read woff above (a wave's LDS accesses complete in
+    // order); the first lane of each bucket advances it
+    asm volatile("" ::: "memory");
+    if (valid && rank == 0) woff[kb] += __popcll(peers);
+    asm volatile("" ::: "memory");
+  }
+}
+
+// ---------------------------------------------------------------------------
 // out[t, d] = sum_j round(scores[t, j] * y[inv[t*k + j], d]), j in order,
 // fp32 sum, one rounding to the output dtype. Rows with inv out of range
 // give NaN. VEC elements per thread (8 when D % 8 == 0).
@@ -214,7 +322,20 @@ size_t moe_sort_lds(int64_t E) {
   return (size_t)(nb + c) * sizeof(int);
 }
 
+// [E + 1] bucket starts, [16 (E + 1)] per-wave offsets, [1024] scan runs
+size_t moe_sort_small_lds(int64_t E) { return (size_t)((E + 1) * (1 + kSortWaves) + kSortThreads) * sizeof(int); }
+
 hipError_t launch_moe_sort(const SortArgs& a) {
+  if (a.n <= kSortSuper) {
+    const size_t lds = moe_sort_small_lds(a.E);
+    static std::atomic<uint64_t> raised_small{0};
+    if (lds > 64 * 1024) {
+      hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(moe_sort_small_kernel), 160 * 1024, raised_small);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(moe_sort_small_kernel, dim3(1), dim3(kSortThreads), lds, a.stream, a);
+    return hipGetLastError();
+  }
   const size_t lds = moe_sort_lds(a.E);
   static std::atomic<uint64_t> raised{0};
   if (lds > 64 * 1024) {

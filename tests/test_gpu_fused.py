@@ -126,7 +126,8 @@ def test_swiglu_elementwise_matches_oracle(dev):
 # --- MoE -----------------------------------------------------------------------
 
 @pytest.mark.parametrize("n,E", [(1, 1), (7, 4), (1000, 8), (1024, 128), (1025, 128),
-                                 (4096, 128), (33000, 512), (5000, 2048)])
+                                 (3000, 2), (4096, 128), (16384, 64), (16385, 64),
+                                 (33000, 512), (5000, 2048)])
 def test_moe_sort_is_the_stable_argsort(dev, n, E):
     rng = np.random.default_rng(n + E)
     k = 8 if n % 8 == 0 else 1
