@@ -75,6 +75,7 @@ hipError_t launch_quantize(const QuantArgs& a);
   hipError_t launch_qmvx_t_b##B(const QArgs& a);         \
   hipError_t launch_gqmm_t_b##B(const QArgs& a);         \
   hipError_t launch_gqms_t_b##B(const QArgs& a);         \
+  hipError_t launch_gqms_dense_t_b##B(const QArgs& a);   \
   hipError_t launch_qmm_t_b##B(const QArgs& a);          \
   hipError_t launch_qmv_n_b##B(const QArgs& a);
 

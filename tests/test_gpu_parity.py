@@ -388,6 +388,23 @@ def test_qmm_mid_rows_on_the_gemm(dev, M, bits, g):
     _sampled_rows_check(dev, M, 1000, 2048, bits, g, seed=M * 13 + bits + g, n_rows=64)
 
 
+@pytest.mark.parametrize("N,K", [(8200, 2048), (9000, 4096)])
+@pytest.mark.parametrize("dt,g", [(O.BF16, 64), (O.F16, 128)])
+def test_qmv_eight_rows_streaming_form(dev, N, K, dt, g):
+    """8 rows of 4-bit weights with many output tiles run on the streaming
+    kernel's batched form (x for the whole K in LDS, two waves per tile);
+    ragged N (the last tile clamped), both 16-bit dtypes, groups 64 and 128;
+    every output row of 96 sampled weight rows vs the oracle."""
+    w, s, b = quant(N + K, N, K, 4, g, dt)
+    x = x_of(N + 1, (8, K), dt)
+    y = ops.quantized_matmul(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                             to_dev(b, dt, dev), True, g, 4)
+    rows = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(N).integers(0, N, 96)]))
+    ref = O.qmm_f64(x, dt, w[rows], s[rows], b[rows], dt, g, 4)
+    got = to_host_f64(y)[:, rows]
+    assert rel_err(got, ref) <= 1e-2
+
+
 # --- prefill GEMM with K split inside the block (few output tiles) -----------
 
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 4000, 1536), (512, 8000, 1024),
