@@ -151,13 +151,19 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(SortArgs a) {
 // then each wave places its elements in order, 64 at a time, with no further
 // barrier (a wave ranks a key among the equal-bucket lanes before it, and the
 // first lane of each bucket advances the wave's offset for that bucket).
+// STAGE (when the LDS holds 8 n more bytes): the placement writes the sorted
+// arrays into LDS, and one coalesced pass copies them out (scattered 4-byte
+// stores from the one workgroup were most of its time).
 // ---------------------------------------------------------------------------
+template <bool STAGE>
 __global__ __launch_bounds__(kSortThreads) void moe_sort_small_kernel(SortArgs a) {
   extern __shared__ int sm[];
   const int NB = a.E + 1;                  // buckets
   int* start = sm;                         // [NB] bucket totals, then starts
   int* cnt = sm + NB;                      // [kSortWaves][NB] per-wave counts, then offsets
   int* runs = cnt + kSortWaves * NB;       // [kSortThreads] scan of per-thread runs
+  uint32_t* ord = reinterpret_cast<uint32_t*>(runs + kSortThreads);  // STAGE: [n] order
+  uint32_t* kv = ord + a.n;                                          // STAGE: [n] sorted indices
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int n = (int)a.n;
   const uint32_t E = (uint32_t)a.E;
@@ -237,16 +243,31 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_small_kernel(SortArgs a
     const int rank = __popcll(peers & lt);
     const int pos = valid ? start[kb] + woff[kb] + rank : 0;
     if (valid) {
-      if (a.order) a.order[pos] = (uint32_t)i;
       if (a.inv_order) a.inv_order[i] = (uint32_t)pos;
-      if (a.idx_sorted) a.idx_sorted[pos] = kb < E ? kb : a.idx[i];
-      if (a.token_idx) a.token_idx[pos] = (uint32_t)(i / a.top_k);
+      const uint32_t sv = kb < E ? kb : a.idx[i];
+      if constexpr (STAGE) {
+        ord[pos] = (uint32_t)i;
+        kv[pos] = sv;
+      } else {
+        if (a.order) a.order[pos] = (uint32_t)i;
+        if (a.idx_sorted) a.idx_sorted[pos] = sv;
+        if (a.token_idx) a.token_idx[pos] = (uint32_t)i / (uint32_t)a.top_k;
+      }
     }
     // every lane has read woff above (a wave's LDS accesses complete in
     // order); the first lane of each bucket advances it
     asm volatile("" ::: "memory");
     if (valid && rank == 0) woff[kb] += __popcll(peers);
     asm volatile("" ::: "memory");
+  }
+  if constexpr (STAGE) {
+    __syncthreads();
+    for (int p = tid; p < n; p += kSortThreads) {
+      const uint32_t i = ord[p];
+      if (a.order) a.order[p] = i;
+      if (a.idx_sorted) a.idx_sorted[p] = kv[p];
+      if (a.token_idx) a.token_idx[p] = i / (uint32_t)a.top_k;
+    }
   }
 }
 
@@ -325,16 +346,22 @@ size_t moe_sort_lds(int64_t E) {
 // [E + 1] bucket starts, [16 (E + 1)] per-wave offsets, [1024] scan runs
 size_t moe_sort_small_lds(int64_t E) { return (size_t)((E + 1) * (1 + kSortWaves) + kSortThreads) * sizeof(int); }
 
+template <bool STAGE>
+hipError_t launch_moe_sort_small(const SortArgs& a, size_t lds) {
+  static std::atomic<uint64_t> raised{0};
+  if (lds > 64 * 1024) {
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(moe_sort_small_kernel<STAGE>), 160 * 1024, raised);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(moe_sort_small_kernel<STAGE>, dim3(1), dim3(kSortThreads), lds, a.stream, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_moe_sort(const SortArgs& a) {
   if (a.n <= kSortSuper) {
-    const size_t lds = moe_sort_small_lds(a.E);
-    static std::atomic<uint64_t> raised_small{0};
-    if (lds > 64 * 1024) {
-      hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(moe_sort_small_kernel), 160 * 1024, raised_small);
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(moe_sort_small_kernel, dim3(1), dim3(kSortThreads), lds, a.stream, a);
-    return hipGetLastError();
+    const size_t lds = moe_sort_small_lds(a.E), staged = lds + (size_t)a.n * 8;
+    if (staged <= 160 * 1024) return launch_moe_sort_small<true>(a, staged);
+    return launch_moe_sort_small<false>(a, lds);
   }
   const size_t lds = moe_sort_lds(a.E);
   static std::atomic<uint64_t> raised{0};
