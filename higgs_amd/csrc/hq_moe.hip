@@ -346,6 +346,7 @@ size_t moe_sort_lds(int64_t E) {
 // [E + 1] bucket starts, [16 (E + 1)] per-wave offsets, [1024] scan runs
 size_t moe_sort_small_lds(int64_t E) { return (size_t)((E + 1) * (1 + kSortWaves) + kSortThreads) * sizeof(int); }
 
+namespace {
 template <bool STAGE>
 hipError_t launch_moe_sort_small(const SortArgs& a, size_t lds) {
   static std::atomic<uint64_t> raised{0};
@@ -356,6 +357,7 @@ hipError_t launch_moe_sort_small(const SortArgs& a, size_t lds) {
   hipLaunchKernelGGL(moe_sort_small_kernel<STAGE>, dim3(1), dim3(kSortThreads), lds, a.stream, a);
   return hipGetLastError();
 }
+}  // namespace
 
 hipError_t launch_moe_sort(const SortArgs& a) {
   if (a.n <= kSortSuper) {
