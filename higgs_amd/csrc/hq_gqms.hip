@@ -29,6 +29,7 @@
 // streams its 16-row W tiles through a register double buffer while it
 // multiplies. The block row e == w_batch fills rows of out-of-range expert
 // indices with NaN, and rows whose x index is out of range are NaN too.
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -585,9 +586,11 @@ hipError_t run_gqms(const QArgs& a) {
   k.nib_mask = 0x000F000Fu;
   k.off_pair = SMma<XDT>::OFFB;
   k.ntiles = (int)((a.N + 15) / 16);
-  // up to 64 weight tiles (16 rows x K) per block; DENSE: the 4 tiles its
-  // waves work on at once
-  k.ns = DENSE ? (k.ntiles + SH::TPW - 1) / SH::TPW : (k.ntiles + 63) / 64;
+  // up to 64 weight tiles (16 rows x K) per block; DENSE: groups of the 4
+  // tiles its waves work on at once, at most one block per CU (the x rows
+  // are staged once per block: lm_head at 8 rows, 2,004 blocks of 4 tiles,
+  // staged them 2,004 times)
+  k.ns = DENSE ? std::min((k.ntiles + SH::TPW - 1) / SH::TPW, device_cu_count()) : (k.ntiles + 63) / 64;
   auto fn = gqms_kernel<XDT, GS, KC, SWI, DENSE>;
   static std::atomic<uint64_t> raised{0};
   hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), lds, raised);

@@ -285,7 +285,11 @@ __device__ __forceinline__ u32x4 deq8(const uint32_t (&wd)[BITS], int qq, float 
   u32x4 h;
   if constexpr (BITS == 4) {
     const uint32_t w = wd[qq];
-    const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;
+    uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;
+    // Opaque to the optimizer: otherwise it folds the masks into per-element
+    // bit-field extracts (v_bfe_u32 + v_cvt_f32_ubyte0, two instructions per
+    // element instead of one v_cvt_f32_ubyteN; 15 % of the 4-bit GEMM loop).
+    asm("" : "+v"(ev), "+v"(od));
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const float q0 = (float)((ev >> (8 * e)) & 0xffu);  // element 2e

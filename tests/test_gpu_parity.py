@@ -388,13 +388,16 @@ def test_qmm_mid_rows_on_the_gemm(dev, M, bits, g):
     _sampled_rows_check(dev, M, 1000, 2048, bits, g, seed=M * 13 + bits + g, n_rows=64)
 
 
-@pytest.mark.parametrize("N,K", [(8200, 2048), (9000, 4096)])
+@pytest.mark.parametrize("N,K", [(8200, 2048), (9000, 4096), (40008, 2048)])
 @pytest.mark.parametrize("dt,g", [(O.BF16, 64), (O.F16, 128)])
 def test_qmv_eight_rows_streaming_form(dev, N, K, dt, g):
     """8 rows of 4-bit weights with many output tiles run on the streaming
     kernel's batched form (x for the whole K in LDS, two waves per tile);
     ragged N (the last tile clamped), both 16-bit dtypes, groups 64 and 128;
-    every output row of 96 sampled weight rows vs the oracle."""
+    N = 40008 gives a block more tile groups than its waves hold at once (2,501
+    tiles over at most one block per CU: a tile count per block that is not a
+    multiple of 4, and blocks past the last tile); every output row of 96
+    sampled weight rows vs the oracle."""
     w, s, b = quant(N + K, N, K, 4, g, dt)
     x = x_of(N + 1, (8, K), dt)
     y = ops.quantized_matmul(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
