@@ -235,6 +235,9 @@ template <int SZ> struct GTile;
 template <> struct GTile<256> {
   static constexpr int TN = 256, TM = 256, WAVES = 8, WN = 128, WM = 64;
 };
+template <> struct GTile<224> {
+  static constexpr int TN = 224, TM = 256, WAVES = 8, WN = 112, WM = 64;
+};
 template <> struct GTile<384> {
   static constexpr int TN = 256, TM = 128, WAVES = 8, WN = 64, WM = 64;
 };
@@ -350,9 +353,13 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   // unconditional.
   constexpr int XJ = GBM / (NT / 8);
   const int xr = tid >> 3, xc = tid & 7;
-  static_assert(GBM == XJ * (NT / 8) && GBN == NT / 2, "thread maps cover the tiles");
-  // W tile (GBN x 64): thread dequantizes pack wp of row wr.
+  static_assert(GBM == XJ * (NT / 8) && GBN <= NT / 2, "thread maps cover the tiles");
+  static_assert(!SWI || NI % 2 == 0, "SwiGLU pairs gate and up fragments");
+  // W tile (GBN x 64): thread dequantizes pack wp of row wr. A tile of fewer
+  // than NT / 2 rows (224) leaves the last threads without a row: they load
+  // the tile's last row (a cache hit) and store nothing.
   const int wr = tid >> 1, wp = tid & 1;
+  const bool w_row = GBN == NT / 2 || wr < GBN;
   uint32_t xoff[XJ];  // element offsets into x (the launcher checks M*K < 2^31)
 #pragma unroll
   for (int j = 0; j < XJ; j++)
@@ -361,7 +368,7 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   // (wr % WN < WN/2) or of the up projection.
   constexpr int HW = TL::WN / 2;
   const bool w_up = SWI && (wr % TL::WN) >= HW;
-  const int wn_row = min(SWI ? n0 + (wr / TL::WN) * HW + (wr % HW) : n0 + wr, N - 1);
+  const int wn_row = min(SWI ? n0 + (wr / TL::WN) * HW + (wr % HW) : n0 + min(wr, GBN - 1), N - 1);
   const uint32_t woff = (uint32_t)((int64_t)wn_row * P) + wp * BITS;
   const uint32_t goff = (uint32_t)((int64_t)wn_row * G);
   const uint32_t* wg = w_up ? a.w2 : a.w;
@@ -383,7 +390,8 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   // Quarter qq (8 elements) of this thread's pack, one 16-byte LDS store.
   auto wchunk = [&](const WPre& p, int buf, int qq) {
     uint16_t* dst = As + buf * GBN * GLD + wr * GLD + wp * 32 + qq * 8;
-    *reinterpret_cast<u32x4*>(dst) = deq8<BITS, CT>(p.wd, qq, DT_<CT>::to_f32(p.sv), DT_<CT>::to_f32(p.bv));
+    const u32x4 v = deq8<BITS, CT>(p.wd, qq, DT_<CT>::to_f32(p.sv), DT_<CT>::to_f32(p.bv));
+    if (w_row) *reinterpret_cast<u32x4*>(dst) = v;
   };
 
   floatx4 acc[NI][NJ];
@@ -412,7 +420,7 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
             *reinterpret_cast<const u32x4*>(as + (wn * TL::WN + i * 16 + (lane & 15)) * GLD + kofs));
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = T::mma(fa, fb[j], acc[i][j]);
-        if (i % (NI / 2) == 0) wchunk(wn_, buf ^ 1, ks * 2 + i / (NI / 2));
+        if (i % ((NI + 1) / 2) == 0) wchunk(wn_, buf ^ 1, ks * 2 + i / ((NI + 1) / 2));
       }
     }
   };
@@ -615,7 +623,17 @@ hipError_t run_qgemm(const QArgs& a) {
   };
   auto tiles = [&](int64_t t) { return tiles2(t, t); };
   const int64_t steps = a.K / GBK;
-  if (tiles(256) >= cus) return run_qgemm_sz<CT, GS, SWI, 256, 1>(a);
+  if (tiles(256) >= cus) {
+    // 224 x 256 tiles when they take fewer rounds of work (7/8 of a 256-tile
+    // each): M = 2048 gate/up, 448 256-tiles (2 rounds on 256 CUs, the
+    // second a quarter empty) against 512 224-tiles (2 full rounds): 265 ->
+    // 252 us on the same box. No SwiGLU form (its fragments pair up).
+    if constexpr (!SWI) {
+      auto rounds = [&](int64_t t) { return (t + cus - 1) / cus; };
+      if (rounds(tiles2(224, 256)) * 7 < rounds(tiles(256)) * 8) return run_qgemm_sz<CT, GS, SWI, 224, 1>(a);
+    }
+    return run_qgemm_sz<CT, GS, SWI, 256, 1>(a);
+  }
   // 256 x 128 before 128 x 128: one 8-wave block per CU instead of two
   // 4-wave blocks, half the x tile loads (M = 2048 down 341 -> 306 us)
   if (tiles2(256, 128) >= cus) return run_qgemm_sz<CT, GS, SWI, 384, 1>(a);

@@ -408,6 +408,15 @@ def test_qmv_eight_rows_streaming_form(dev, N, K, dt, g):
     assert rel_err(got, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("bits,g", [(4, 64), (3, 32), (8, 128), (2, 64)])
+def test_qgemm_224_row_tiles(dev, bits, g):
+    """A product whose 256 x 256 tiles would leave the last round of CUs part
+    empty runs on 224 x 256 tiles (the last 32 threads' W rows unused): N not
+    a multiple of 224 and M not of 256 (ragged tiles both ways); sampled rows
+    vs the oracle."""
+    _sampled_rows_check(dev, 1100, 14000, 1024, bits, g, seed=224 + bits + g, n_rows=96)
+
+
 # --- prefill GEMM with K split inside the block (few output tiles) -----------
 
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 4000, 1536), (512, 8000, 1024),
