@@ -241,6 +241,9 @@ template <> struct GTile<224> {
 template <> struct GTile<384> {
   static constexpr int TN = 256, TM = 128, WAVES = 8, WN = 64, WM = 64;
 };
+template <> struct GTile<96> {
+  static constexpr int TN = 96, TM = 128, WAVES = 4, WN = 48, WM = 64;
+};
 template <> struct GTile<128> {
   static constexpr int TN = 128, TM = 128, WAVES = 4, WN = 64, WM = 64;
 };
@@ -623,13 +626,13 @@ hipError_t run_qgemm(const QArgs& a) {
   };
   auto tiles = [&](int64_t t) { return tiles2(t, t); };
   const int64_t steps = a.K / GBK;
+  auto rounds = [&](int64_t t) { return (t + cus - 1) / cus; };
   if (tiles(256) >= cus) {
     // 224 x 256 tiles when they take fewer rounds of work (7/8 of a 256-tile
     // each): M = 2048 gate/up, 448 256-tiles (2 rounds on 256 CUs, the
     // second a quarter empty) against 512 224-tiles (2 full rounds): 265 ->
     // 252 us on the same box. No SwiGLU form (its fragments pair up).
     if constexpr (!SWI) {
-      auto rounds = [&](int64_t t) { return (t + cus - 1) / cus; };
       if (rounds(tiles2(224, 256)) * 7 < rounds(tiles(256)) * 8) return run_qgemm_sz<CT, GS, SWI, 224, 1>(a);
     }
     return run_qgemm_sz<CT, GS, SWI, 256, 1>(a);
@@ -638,8 +641,16 @@ hipError_t run_qgemm(const QArgs& a) {
   // 4-wave blocks, half the x tile loads (M = 2048 down 341 -> 306 us)
   if (tiles2(256, 128) >= cus) return run_qgemm_sz<CT, GS, SWI, 384, 1>(a);
   if (tiles(128) >= cus) return run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
-  if (2 * tiles(128) >= cus)
+  if (2 * tiles(128) >= cus) {
+    // 96 x 128 tiles (3/4 of a 128-tile each) when they fill the CUs in as
+    // few rounds: configs[3] gate/up has 192 128-tiles (a quarter of the
+    // CUs idle) against 256 96-tiles. No SwiGLU form (its fragments pair up).
+    if constexpr (!SWI) {
+      if (steps % 2 == 0 && rounds(tiles2(96, 128)) * 3 < rounds(tiles(128)) * 4)
+        return run_qgemm_sz<CT, GS, SWI, 96, 2>(a);
+    }
     return steps % 2 == 0 ? run_qgemm_sz<CT, GS, SWI, 128, 2>(a) : run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
+  }
   const int64_t t64 = tiles(64);
   if (t64 <= cus && steps % 4 == 0) return run_qgemm_sz<CT, GS, SWI, 64, 4>(a);
   if (t64 <= 2 * cus && steps % 2 == 0) return run_qgemm_sz<CT, GS, SWI, 64, 2>(a);

@@ -417,6 +417,15 @@ def test_qgemm_224_row_tiles(dev, bits, g):
     _sampled_rows_check(dev, 1100, 14000, 1024, bits, g, seed=224 + bits + g, n_rows=96)
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 6000, 1024), (512, 6144, 2048)])
+@pytest.mark.parametrize("bits,g", [(4, 64), (3, 32), (8, 128), (2, 64)])
+def test_qgemm_96_row_tiles(dev, M, N, K, bits, g):
+    """Products whose 128 x 128 split-K tiles would leave CUs idle run on
+    96 x 128 tiles (the last 32 threads' W rows unused): ragged N and M, and
+    the configs[3] gate/up shape; sampled rows vs the oracle."""
+    _sampled_rows_check(dev, M, N, K, bits, g, seed=96 + M + bits + g, n_rows=96)
+
+
 # --- prefill GEMM with K split inside the block (few output tiles) -----------
 
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 4000, 1536), (512, 8000, 1024),
