@@ -299,8 +299,16 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
     // the compiled code).
     issue_sb(ba, 0);
     __builtin_amdgcn_sched_barrier(0);
+    // DENSE: slots k >= 1 past the last row are not staged (their MFMA rows
+    // are never stored, and their sums are skipped), so 8 rows stage half of
+    // the 16 slots. They go first, so the last DMA (slot 0, always staged)
+    // is followed by straight-line code up to the wait. (The grouped form
+    // keeps every slot: there the x row offsets come from loaded indices,
+    // and a skipped DMA made the compiler wait for every load at the join.)
 #pragma unroll
-    for (int k = 0; k < RPW; k++) {
+    for (int kk = 0; kk < RPW; kk++) {
+      const int k = DENSE ? RPW - 1 - kk : kk;
+      if (DENSE && k > 0 && wv + 8 * k >= nrows) continue;
       const XS* src = (const XS*)a.x + xoff[k] + lane * 8;
       uint16_t* dst = xs + xrow_off(wv + 8 * k, KK);
 #pragma unroll
