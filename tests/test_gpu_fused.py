@@ -82,6 +82,17 @@ def test_dense_hidden_fused_f16(dev, M):
     assert rel_err(to_host_f64(h), ref) <= 1e-2
 
 
+def test_fused_swiglu_on_64x128_tiles(dev):
+    """100 rows against 6000 gate/up columns: the fused GEMM on 64 x 128
+    tiles with split-K (32 output columns per tile, ragged N and M)."""
+    M, N, K, dt, bits, g = 100, 6000, 1024, O.BF16, 4, 64
+    x, w, s, b = _dense_case(640 + M, M, N, K, bits, g, dt)
+    h = ops.dense_hidden_fused(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                               to_dev(b, dt, dev), N, g, bits)
+    ref = _swiglu_ref(x, dt, w[:N], s[:N], b[:N], w[N:], s[N:], b[N:], g, bits)
+    assert rel_err(to_host_f64(h), ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 256])
 def test_fused_equals_separate(dev, M):
     # qwen3_next.rs:13132-13169: fused gate||up == separate projections

@@ -426,6 +426,15 @@ def test_qgemm_96_row_tiles(dev, M, N, K, bits, g):
     _sampled_rows_check(dev, M, N, K, bits, g, seed=96 + M + bits + g, n_rows=96)
 
 
+@pytest.mark.parametrize("M", [65, 100, 128])
+@pytest.mark.parametrize("bits,g", [(4, 64), (3, 32), (8, 128)])
+def test_qgemm_64x128_tiles(dev, M, bits, g):
+    """65-128 rows against many W rows run on 64 x 128 tiles with K split
+    over 2 wave groups (half the threads without a W row): ragged N and M;
+    sampled rows vs the oracle."""
+    _sampled_rows_check(dev, M, 14000, 1024, bits, g, seed=192 + M + bits + g, n_rows=96)
+
+
 # --- prefill GEMM with K split inside the block (few output tiles) -----------
 
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 4000, 1536), (512, 8000, 1024),
