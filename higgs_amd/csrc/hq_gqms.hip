@@ -681,7 +681,10 @@ hipError_t HQ_CAT(launch_gqms_dense_t_b, HQ_BITS)(const QArgs& a) {
   } else {
     if (a.w2 || a.lb || a.lhs || a.rhs || a.batch != 1 || a.xdt != a.sdt || a.xdt == DT_F32)
       return hipErrorNotSupported;
-    if (a.M < 8 || a.M > 16 || a.N < 8192 || a.N > ((int64_t)1 << 30)) return hipErrorNotSupported;
+    // 4-7 rows only at vocabulary-sized N (its cost hardly depends on the
+    // row count: below 8 rows the GEMV kernels win on smaller N)
+    if (a.M < (a.N >= 65536 ? 4 : 8) || a.M > 16 || a.N < 8192 || a.N > ((int64_t)1 << 30))
+      return hipErrorNotSupported;
     if (a.group_size != 64 && a.group_size != 128) return hipErrorNotSupported;
     if (!aligned16(a.s) || !aligned16(a.b)) return hipErrorNotSupported;
     QArgs d = a;

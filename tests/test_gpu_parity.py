@@ -435,6 +435,21 @@ def test_qgemm_64x128_tiles(dev, M, bits, g):
     _sampled_rows_check(dev, M, 14000, 1024, bits, g, seed=192 + M + bits + g, n_rows=96)
 
 
+@pytest.mark.parametrize("M", [4, 5])
+def test_qmv_few_rows_vocabulary_dense_form(dev, M):
+    """4-7 rows against a vocabulary-sized N run on the streaming kernel's
+    dense form (16 row slots, only M of them staged); 66,000 rows give 17
+    tiles per block; sampled weight rows vs the oracle."""
+    N, K, dt, g = 66000, 2048, O.BF16, 64
+    w, s, b = quant(N + M, N, K, 4, g, dt)
+    x = x_of(M, (M, K), dt)
+    y = ops.quantized_matmul(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                             to_dev(b, dt, dev), True, g, 4)
+    rows = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(N + M).integers(0, N, 96)]))
+    ref = O.qmm_f64(x, dt, w[rows], s[rows], b[rows], dt, g, 4)
+    assert rel_err(to_host_f64(y)[:, rows], ref) <= 1e-2
+
+
 # --- prefill GEMM with K split inside the block (few output tiles) -----------
 
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 4000, 1536), (512, 8000, 1024),
