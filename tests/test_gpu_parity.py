@@ -410,19 +410,18 @@ def test_qmv_eight_rows_streaming_form(dev, N, K, dt, g):
 
 @pytest.mark.parametrize("bits,g", [(4, 64), (3, 32), (8, 128), (2, 64)])
 def test_qgemm_224_row_tiles(dev, bits, g):
-    """A product whose 256 x 256 tiles would leave the last round of CUs part
-    empty runs on 224 x 256 tiles (the last 32 threads' W rows unused): N not
-    a multiple of 224 and M not of 256 (ragged tiles both ways); sampled rows
-    vs the oracle."""
-    _sampled_rows_check(dev, 1100, 14000, 1024, bits, g, seed=224 + bits + g, n_rows=96)
+    """A product the tile cost model gives 224 x 256 tiles (the last 32
+    threads' W rows unused): N not a multiple of 224 and M not of 256 (ragged
+    tiles both ways); sampled rows vs the oracle."""
+    _sampled_rows_check(dev, 544, 13321, 1024, bits, g, seed=224 + bits + g, n_rows=96)
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 6000, 1024), (512, 6144, 2048)])
+@pytest.mark.parametrize("M,N,K", [(137, 10990, 1024), (512, 6144, 2048)])
 @pytest.mark.parametrize("bits,g", [(4, 64), (3, 32), (8, 128), (2, 64)])
 def test_qgemm_96_row_tiles(dev, M, N, K, bits, g):
-    """Products whose 128 x 128 split-K tiles would leave CUs idle run on
-    96 x 128 tiles (the last 32 threads' W rows unused): ragged N and M, and
-    the configs[3] gate/up shape; sampled rows vs the oracle."""
+    """Products the tile cost model gives 96 x 128 split-K tiles (the last 32
+    threads' W rows unused): ragged N and M, and the configs[3] gate/up
+    shape; sampled rows vs the oracle."""
     _sampled_rows_check(dev, M, N, K, bits, g, seed=96 + M + bits + g, n_rows=96)
 
 
@@ -448,6 +447,19 @@ def test_qmv_few_rows_vocabulary_dense_form(dev, M):
     rows = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(N + M).integers(0, N, 96)]))
     ref = O.qmm_f64(x, dt, w[rows], s[rows], b[rows], dt, g, 4)
     assert rel_err(to_host_f64(y)[:, rows], ref) <= 1e-2
+
+
+@pytest.mark.parametrize("M,N,K,bits,g", [
+    (M, N, K, bits, g)
+    for (M, N, K) in [(803, 14653, 1024), (285, 10990, 1024), (803, 9325, 1024),
+                      (137, 12322, 1024), (137, 8326, 1024), (100, 1000, 1088)]
+    for (bits, g) in [(4, 64), (3, 32), (8, 128)] if K % g == 0])
+def test_qgemm_every_tile_form(dev, M, N, K, bits, g):
+    """The tile cost model's other forms, each on a shape that picks it with
+    ragged N and M (on 256 CUs): 256 x 256, 256 x 128, 128 x 128 without and
+    with split-K, 64 x 64 with K split over 2 groups, and 64 x 64 without
+    split-K (K / 64 odd, so no group of 128); sampled rows vs the oracle."""
+    _sampled_rows_check(dev, M, N, K, bits, g, seed=M + N + K + 7 * bits, n_rows=96)
 
 
 # --- prefill GEMM with K split inside the block (few output tiles) -----------
