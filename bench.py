@@ -23,6 +23,8 @@ Printed JSON line (one, on stdout):
                 and fused gate/up + SwiGLU), GB/s and fraction of HBM peak
   qmm           configs[2]: M = 2048 prefill GEMMs, TFLOP/s and fraction of
                 the 2.5 PFLOP/s dense bf16 MFMA peak
+  prefill_chunks  the Llama-3-8B q/o, k/v, gate/up and down products at
+                M = 512 and 1024 rows (chunked prefill), TFLOP/s
   moe           configs[4]: sorted gather_qmm (gate, down) at the MoE shapes,
                 and the whole expert block on device (sort, fused gate/up +
                 SwiGLU, down, unsort + score-weighted combine)
@@ -242,6 +244,39 @@ def bench_qmm(model, dev, steps):
         tflops = 2.0 * 2048 * N * K / (ms * 1e-3) / 1e12
         out[name] = {"M": 2048, "N": N, "K": K, "us": round(ms * 1e3, 2),
                      "tflops": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+    return out
+
+
+def bench_prefill_chunks(dev, steps):
+    """Chunked prefill (higgs prefills in chunks of at most 512 tokens, and a
+    batch engine can exceed that): the Llama-3-8B projections at M = 512 and
+    1024 rows, each over >= 1 GiB of distinct weight copies; TFLOP/s and the
+    fraction of the 2.5 PFLOP/s bf16 peak."""
+    import torch
+
+    from higgs_amd import _lib, gen
+
+    lib = _lib.lib()
+    out = {}
+    for name, N, K in (("q_o", HIDDEN, HIDDEN), ("k_v", 1024, HIDDEN), ("gate_up", INTER, HIDDEN),
+                       ("down", HIDDEN, INTER)):
+        ws = [gen.torch_quantized(700 + c, N, K, BITS, GROUP, dev) for c in range(rotation(N, K))]
+        for M in (512, 1024):
+            x = gen.torch_x(701, (M, K), dev)
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+            def run(stream, ws=ws, x=x, y=y, M=M, N=N, K=K):
+                for (w, s, b) in ws:
+                    _lib.check(lib.hq_quantized_matmul(y.data_ptr(), x.data_ptr(), w.data_ptr(),
+                                                       s.data_ptr(), b.data_ptr(), M, N, K, 1,
+                                                       GROUP, BITS, 2, 2, stream))
+            ms = time_graph(run, steps, 1, dev) / len(ws)
+            tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+            out[f"{name}_M{M}"] = {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                                   "tflops": round(tflops, 1),
+                                   "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+        del ws
+        torch.cuda.empty_cache()
     return out
 
 
@@ -617,8 +652,8 @@ def bench_fused(model, args, dev):
     return r
 
 
-SECTIONS = ("qmv_shapes", "qmv_batch", "mid_rows", "qmm", "moe", "configs", "dequant",
-            "decode_fused")
+SECTIONS = ("qmv_shapes", "qmv_batch", "mid_rows", "qmm", "prefill_chunks", "moe", "configs",
+            "dequant", "decode_fused")
 
 
 def sections(model, args, step, dev):
@@ -629,6 +664,7 @@ def sections(model, args, step, dev):
         "qmv_batch": lambda: bench_batch(model, args, step, dev),
         "mid_rows": lambda: bench_mid_rows(model, dev, sub),
         "qmm": lambda: bench_qmm(model, dev, sub),
+        "prefill_chunks": lambda: bench_prefill_chunks(dev, sub),
         "moe": lambda: bench_moe(dev, sub),
         "configs": lambda: bench_configs(dev, sub),
         "dequant": lambda: bench_dequant(dev, sub),
