@@ -612,24 +612,25 @@ hipError_t run_qgemm_sz(const QArgs& a) {
   return hipGetLastError();
 }
 
-// Tile choice. The plain product uses a cost model: the CU that runs the
-// most tiles sets the time, so cost = ceil(tiles / CUs) x (MFMA work of a
-// tile) / (throughput of that tile form relative to the 256 x 256 tile).
+// Tile choice by a cost model: the CU that runs the most tiles sets the
+// time, so cost = ceil(tiles / CUs) x (MFMA work of a tile) / (throughput of
+// that tile form relative to the 256 x 256 tile); the cheapest form runs.
 // The relative throughputs were fitted to same-box measurements on random
-// 4-bit g64 data, and the model picks the fastest measured form on every
-// one of them (us, chosen form first): Llama-3-8B gate/up 14336 x 4096 at
+// 4-bit g64 data, and the model picks the fastest measured form on every one
+// of them (us, chosen form first): Llama-3-8B gate/up 14336 x 4096 at
 // M = 2048 224x256 252-256 vs 256x256 265; M = 1024 224x256 127-134 vs
 // 256x128 171; M = 256 128/2 54-56 vs 64x128/2 76, 96/2 89; down
 // 4096 x 14336 at M = 1024 128/2 180 vs 128/1 235, 256x128 267; M = 512
 // 64x128/2 126 vs 96/2 150, 128/2 164; q/o 4096 x 4096 at M = 1024 128/2
 // 53 vs 128/1 71; M = 512 64x128/2 39 vs 96/2 47, 64/4 48; M = 127 at
 // 14336 x 4096 64x128/2 39 vs 64/2 46; configs[3] gate/up 96/2 26.5 vs
-// 128/2 28.7; configs[3] down 64/4 36 vs 64/2 49. (x/y: K split over y
-// wave groups inside the block; 256x128 is id 384, 64x128 id 192.) A
-// 128 x 128 tile without split-K has 4 waves: it keeps up only with a
-// second block on the CU. The fused SwiGLU keeps the rules below the model
-// (largest tile that gives every CU one, then split-K), measured on its own
-// shapes.
+// 128/2 28.7; configs[3] down 64/4 36 vs 64/2 49; the fused gate/up +
+// SwiGLU (2 x 14336 x 4096) at M = 512 256x256 141 vs 256x128 176, M = 256
+// 256x128 90 vs 128/1 100, M = 64 64/2 50 vs 128/2 56, M = 768 256x128 253
+// vs 256x256 263. (x/y: K split over y wave groups inside the block;
+// 256x128 is id 384, 64x128 id 192.) A 128 x 128 tile without split-K has
+// 4 waves: it keeps up only with a second block on the CU. The SwiGLU form
+// has no 224 x 256 or 96 x 128 tiles (its gate and up fragments pair up).
 template <int CT, int GS, bool SWI>
 hipError_t run_qgemm(const QArgs& a) {
   const int cus = device_cu_count();
@@ -639,55 +640,45 @@ hipError_t run_qgemm(const QArgs& a) {
   };
   auto tiles = [&](int64_t t) { return tiles2(t, t); };
   const int64_t steps = a.K / GBK;
-  if constexpr (!SWI) {
-    enum { C256, C224, C384, C128x2, C128x1, C96x2, C192x2, C64x4, C64x2, C64x1 };
-    double best = 0.0;
-    int pick = -1;
-    auto consider = [&](int c, int64_t t, double work, double eff, bool ok) {
-      if (!ok) return;
-      const double cost = (double)((t + cus - 1) / cus) * work / eff;
-      if (pick < 0 || cost < best) {
-        best = cost;
-        pick = c;
-      }
-    };
-    const int64_t t128 = tiles(128), t64 = tiles(64);
-    consider(C256, tiles(256), 65536, 1.00, true);
-    consider(C224, tiles2(224, 256), 57344, 0.91, true);
-    consider(C384, tiles2(256, 128), 32768, 0.78, true);
-    consider(C128x2, t128, 16384, 0.58, steps % 2 == 0);
-    consider(C128x1, t128, 16384, t128 > cus ? 0.69 : 0.44, true);
-    consider(C96x2, tiles2(96, 128), 12288, 0.47, steps % 2 == 0);
-    consider(C192x2, tiles2(64, 128), 8192, 0.37, steps % 2 == 0);
-    consider(C64x4, t64, 4096, 0.30, steps % 4 == 0);
-    consider(C64x2, t64, 4096, t64 > cus ? 0.32 : 0.20, steps % 2 == 0);
-    consider(C64x1, t64, 4096, 0.16, true);
-    switch (pick) {
-      case C256: return run_qgemm_sz<CT, GS, SWI, 256, 1>(a);
-      case C224: return run_qgemm_sz<CT, GS, SWI, 224, 1>(a);
-      case C384: return run_qgemm_sz<CT, GS, SWI, 384, 1>(a);
-      case C128x2: return run_qgemm_sz<CT, GS, SWI, 128, 2>(a);
-      case C128x1: return run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
-      case C96x2: return run_qgemm_sz<CT, GS, SWI, 96, 2>(a);
-      case C192x2: return run_qgemm_sz<CT, GS, SWI, 192, 2>(a);
-      case C64x4: return run_qgemm_sz<CT, GS, SWI, 64, 4>(a);
-      case C64x2: return run_qgemm_sz<CT, GS, SWI, 64, 2>(a);
-      default: return run_qgemm_sz<CT, GS, SWI, 64, 1>(a);
+  enum { C256, C224, C384, C128x2, C128x1, C96x2, C192x2, C64x4, C64x2, C64x1 };
+  double best = 0.0;
+  int pick = -1;
+  auto consider = [&](int c, int64_t t, double work, double eff, bool ok) {
+    if (!ok) return;
+    const double cost = (double)((t + cus - 1) / cus) * work / eff;
+    if (pick < 0 || cost < best) {
+      best = cost;
+      pick = c;
     }
-  } else {
-    if (tiles(256) >= cus) return run_qgemm_sz<CT, GS, SWI, 256, 1>(a);
-    // 256 x 128 before 128 x 128: one 8-wave block per CU instead of two
-    // 4-wave blocks, half the x tile loads
-    if (tiles2(256, 128) >= cus) return run_qgemm_sz<CT, GS, SWI, 384, 1>(a);
-    if (tiles(128) >= cus) return run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
-    if (2 * tiles(128) >= cus)
-      return steps % 2 == 0 ? run_qgemm_sz<CT, GS, SWI, 128, 2>(a) : run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
-    const int64_t t64 = tiles(64);
-    if (t64 <= cus && steps % 4 == 0) return run_qgemm_sz<CT, GS, SWI, 64, 4>(a);
-    if (tiles2(64, 128) <= cus && steps % 2 == 0) return run_qgemm_sz<CT, GS, SWI, 192, 2>(a);
-    if (t64 <= 2 * cus && steps % 2 == 0) return run_qgemm_sz<CT, GS, SWI, 64, 2>(a);
-    return run_qgemm_sz<CT, GS, SWI, 64, 1>(a);
+  };
+  const int64_t t128 = tiles(128), t64 = tiles(64);
+  consider(C256, tiles(256), 65536, 1.00, true);
+  consider(C224, tiles2(224, 256), 57344, 0.91, !SWI);
+  consider(C384, tiles2(256, 128), 32768, 0.78, true);
+  consider(C128x2, t128, 16384, 0.58, steps % 2 == 0);
+  consider(C128x1, t128, 16384, t128 > cus ? 0.69 : 0.44, true);
+  consider(C96x2, tiles2(96, 128), 12288, 0.47, !SWI && steps % 2 == 0);
+  consider(C192x2, tiles2(64, 128), 8192, 0.37, steps % 2 == 0);
+  consider(C64x4, t64, 4096, 0.30, steps % 4 == 0);
+  consider(C64x2, t64, 4096, t64 > cus ? 0.32 : 0.20, steps % 2 == 0);
+  consider(C64x1, t64, 4096, 0.16, true);
+  switch (pick) {
+    case C256: return run_qgemm_sz<CT, GS, SWI, 256, 1>(a);
+    case C224:
+      if constexpr (!SWI) return run_qgemm_sz<CT, GS, SWI, 224, 1>(a);
+      break;
+    case C384: return run_qgemm_sz<CT, GS, SWI, 384, 1>(a);
+    case C128x2: return run_qgemm_sz<CT, GS, SWI, 128, 2>(a);
+    case C128x1: return run_qgemm_sz<CT, GS, SWI, 128, 1>(a);
+    case C96x2:
+      if constexpr (!SWI) return run_qgemm_sz<CT, GS, SWI, 96, 2>(a);
+      break;
+    case C192x2: return run_qgemm_sz<CT, GS, SWI, 192, 2>(a);
+    case C64x4: return run_qgemm_sz<CT, GS, SWI, 64, 4>(a);
+    case C64x2: return run_qgemm_sz<CT, GS, SWI, 64, 2>(a);
+    default: break;
   }
+  return run_qgemm_sz<CT, GS, SWI, 64, 1>(a);
 }
 
 template <int CT, bool SWI = false>

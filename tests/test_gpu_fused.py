@@ -93,6 +93,21 @@ def test_fused_swiglu_on_64x128_tiles(dev):
     assert rel_err(to_host_f64(h), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("M", [64, 256, 512])
+def test_fused_swiglu_gemm_tile_forms(dev, M):
+    """The fused GEMM's tile forms at 14000 gate/up columns (ragged): 64 x 64
+    with split-K (M = 64), 256 x 128 (M = 256) and 256 x 256 (M = 512), as
+    the tile cost model picks them on 256 CUs; 96 sampled output columns vs
+    the oracle."""
+    N, K, dt, bits, g = 14000, 1024, O.BF16, 4, 64
+    x, w, s, b = _dense_case(900 + M, M, N, K, bits, g, dt)
+    h = ops.dense_hidden_fused(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                               to_dev(b, dt, dev), N, g, bits)
+    cols = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(M).integers(0, N, 96)]))
+    ref = _swiglu_ref(x, dt, w[cols], s[cols], b[cols], w[N + cols], s[N + cols], b[N + cols], g, bits)
+    assert rel_err(to_host_f64(h)[:, cols], ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 256])
 def test_fused_equals_separate(dev, M):
     # qwen3_next.rs:13132-13169: fused gate||up == separate projections
