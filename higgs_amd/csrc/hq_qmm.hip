@@ -227,10 +227,11 @@ namespace {
 constexpr int GBM = 256, GBN = 256, GBK = 64;
 
 // Tile shapes of the large-tile GEMM: a block computes TN W rows x TM x rows
-// with WAVES waves of WN x WM each. 256 x 256 (8 waves, one block per CU) is
-// the main shape; 256 x 128 (id 384, 8 waves) and 128 x 128 (4 waves, two
-// blocks per CU) are for products whose 256-tiles would leave CUs idle
-// (M = 2048 down: 128 256-tiles for 256 CUs).
+// with WAVES waves of WN x WM each (times KS wave groups with split-K). The
+// id is the template key: 256 x 256 and 224 x 256 (8 waves, one block per
+// CU; 224 leaves the last 32 threads without a W row), 256 x 128 (id 384, 8
+// waves), 128 x 128 (4 waves), 96 x 128 (id 96), 64 x 128 (id 192) and
+// 64 x 64; run_qgemm picks one by its cost model.
 template <int SZ> struct GTile;
 template <> struct GTile<256> {
   static constexpr int TN = 256, TM = 256, WAVES = 8, WN = 128, WM = 64;
