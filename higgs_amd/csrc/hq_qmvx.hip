@@ -721,12 +721,15 @@ struct SKern {
   const void* s2;
   const void* b2;
   int M, N, K;
-  int ntiles;   // ceil(N / 16)
+  int ntiles;   // ceil(N / TR)
   uint32_t nib_mask, off_pair;
   const void* lb;  // linear bias [N] or null (not with SwiGLU)
 };
 
-template <int BITS, int XDT, int GS, int MB, int TPB, int RW, bool SWI, bool SPLIT, int S, bool XF>
+// TR: W rows per tile, 16, or 8 to spread few W rows over more blocks (the
+// MFMA's other 8 columns repeat them and are not stored).
+template <int BITS, int XDT, int GS, int MB, int TPB, int RW, bool SWI, bool SPLIT, int S, bool XF,
+          int TR = 16>
 __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
   static_assert(S == 4 || S == 8, "a K range is 512 or 1024 elements");  // S: segments per range
   constexpr int H = SWI ? 2 : 1;                     // halves (gate, up)
@@ -777,7 +780,7 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
   };
   // item i: tile t0 + i / (H*RW), half (i / RW) % H, range wv*RW + i % RW
   auto issue = [&](Item& r, int t, int h, int seg_base) {
-    const int n = min(t * 16 + nl, N - 1);
+    const int n = min(t * TR + (nl & (TR - 1)), N - 1);
     const uint32_t* wp = (h ? a.w2 : a.w) + (int64_t)n * P + (int64_t)(seg_base * 4 + q) * BITS;
 #pragma unroll
     for (int u = 0; u < S; u++) load_pack<BITS>(wp + u * 4 * BITS, r.wd[u]);
@@ -982,8 +985,8 @@ __global__ __launch_bounds__(512) void qmvs_kernel(SKern a) {
       }
       float o = hs[0];
       if constexpr (SWI) o = swiglu_f32(DT_<XDT>::round(hs[0]), DT_<XDT>::round(hs[1]));
-      if (tid < M * 16 && t * 16 + (tid & 15) < N) {
-        const int n = t * 16 + (tid & 15);
+      if (tid < M * 16 && (tid & 15) < TR && t * TR + (tid & 15) < N) {
+        const int n = t * TR + (tid & 15);
         ((st_t<XDT>*)a.y)[(int64_t)(tid >> 4) * N + n] =
             SWI ? DT_<XDT>::from_f32(o) : linear_out<XDT>(o, a.lb, n);
       }
@@ -1004,15 +1007,26 @@ hipError_t run_qmvs(const QArgs& a) {
   k.y = a.y; k.x = a.x; k.w = a.w; k.s = a.s; k.b = a.b;
   k.w2 = a.w2; k.s2 = a.s2; k.b2 = a.b2;
   k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
-  k.ntiles = (int)((a.N + 15) / 16);
   k.nib_mask = 0x000F000Fu;
   k.off_pair = XMma<XDT>::OFFB;
   k.lb = a.lb;
+  // 8-row tiles at 4 and 8 x rows when 16-row tiles would occupy at most a
+  // quarter of the CUs (k/v, 1024 x 4096: 128 blocks of 8 rows instead of 64
+  // of 16: 4.61 -> 4.36 us at 4 rows, 5.93 -> 5.12 us at 8; at 1 row it was
+  // slower, 3.76 -> 3.85 us)
+  bool half = false;
+  if constexpr (MB >= 4 && TPB == 1 && !SWI) half = (a.N + 15) / 16 <= device_cu_count() / 4;
+  const int tr = half ? 8 : 16;
+  k.ntiles = (int)((a.N + tr - 1) / tr);
   const int grid = (k.ntiles + TPB - 1) / TPB;
-  auto fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true, S, XF>;
+  auto fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true, S, XF, 16>;
+  if constexpr (MB >= 4 && TPB == 1 && !SWI) {
+    if (half) fn = qmvs_kernel<HQ_BITS, XDT, GS, MB, TPB, RW, SWI, true, S, XF, 8>;
+  }
   if (lds > 64 * 1024) {
-    static std::atomic<uint64_t> raised{0};
-    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), 160 * 1024, raised);
+    // one flag per kernel (the 8- and 16-row forms are separate functions)
+    static std::atomic<uint64_t> raised16{0}, raised8{0};
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(fn), 160 * 1024, half ? raised8 : raised16);
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * W), lds, a.stream, k);
