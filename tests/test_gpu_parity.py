@@ -462,6 +462,15 @@ def test_qgemm_every_tile_form(dev, M, N, K, bits, g):
     _sampled_rows_check(dev, M, N, K, bits, g, seed=M + N + K + 7 * bits, n_rows=96)
 
 
+@pytest.mark.parametrize("M", [4, 8])
+@pytest.mark.parametrize("N", [1003, 520])
+def test_qmv_few_w_rows_eight_row_tiles(dev, M, N):
+    """4 and 8 x rows against at most 1024 W rows run the streaming GEMV on
+    8-row tiles (the MFMA's other 8 columns repeat them, unstored): ragged
+    last tile; every row vs the oracle."""
+    _sampled_rows_check(dev, M, N, 4096, 4, 64, seed=N + 8 * M, n_rows=N)
+
+
 # --- prefill GEMM with K split inside the block (few output tiles) -----------
 
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 4000, 1536), (512, 8000, 1024),
