@@ -11,6 +11,8 @@
 // bf16 x and scales, fp16 likewise, fp32 (16x16x4 fp32 MFMA) otherwise, all
 // with fp32 accumulation. Gathered batches (gather_qmm with M > 8) use
 // blockIdx.z.
+#include <algorithm>
+
 #include "hq_common.hpp"
 #include "hq_device.hpp"
 #include "hq_kernels.hpp"
@@ -975,8 +977,44 @@ hipError_t HQ_CAT(launch_qmm_t_b, HQ_BITS)(const QArgs& a) {
   // (the large-tile GEMM addresses x and W with 32-bit element offsets)
   const bool off32 = a.M * a.K < ((int64_t)1 << 31) &&
                      a.N * (a.K / 32) * HQ_BITS < ((int64_t)1 << 31);
-  if (a.batch == 1 && !a.lhs && !a.rhs && a.xdt == a.sdt && a.xdt != DT_F32 &&
-      a.K % GBK == 0 && a.M > kQmvMaxM && off32) {
+  // 9-16 rows of 4-bit weights with many output tiles: the streaming
+  // kernel's dense form (hq_gqms.hip, its own conditions)
+  if (a.M <= 16 && !a.w2) {
+    const hipError_t ed = HQ_CAT(launch_gqms_dense_t_b, HQ_BITS)(a);
+    if (ed != hipErrorNotSupported) return ed;
+  }
+  const bool gemm_ok = a.batch == 1 && !a.lhs && !a.rhs && a.xdt == a.sdt && a.xdt != DT_F32 &&
+                       a.K % GBK == 0 && a.M > kQmvMaxM && off32;
+  // 9-32 rows on few output tiles: the GEMM's blocks then each stream a
+  // 64-row W slice through a latency-bound K loop (~5.5 ns per K element,
+  // 23 us at K = 4096 whatever N and M), while an 8-row GEMV launch streams
+  // W at ~1.4 TB/s with a ~4.5 us floor. Run ceil(M / 8) GEMV launches
+  // when that model says they are faster. Measured (4-bit g64, us, GEMM vs
+  // GEMV launches): 1024 x 4096 M = 32 23.6 vs 19.0, M = 48 23.9 vs 28.3;
+  // 4096 x 4096 M = 24 23.8 vs 17.3; 4096 x 14336 M = 16 74.3 vs 44.3,
+  // M = 24 75.1 vs 65.8, M = 32 75.9 vs 87.4; 6144 x 4096 M = 16 23.8 vs
+  // 18.0, M = 24 24.0 vs 26.5.
+  if (gemm_ok && !a.w2 && a.M <= 4 * kQmvMaxM) {
+    const int64_t launches = (a.M + kQmvMaxM - 1) / kQmvMaxM;
+    const double w_mb = (double)a.N * (double)a.K * HQ_BITS / 8e6;
+    const double t_gemv = std::max(4.5, w_mb / 1.4);
+    const int64_t cus = device_cu_count();
+    const int64_t rounds = ((a.N + 63) / 64 + cus - 1) / cus;
+    const double t_gemm = (double)rounds * 0.0055 * (double)a.K;
+    if ((double)launches * t_gemv < t_gemm) {
+      const size_t xb = 2, yb = 2;  // same 16-bit dtype for x, scales and y
+      QArgs c = a;
+      hipError_t e = hipSuccess;
+      for (int64_t m0 = 0; m0 < a.M && e == hipSuccess; m0 += kQmvMaxM) {
+        c.M = std::min<int64_t>(a.M - m0, kQmvMaxM);
+        c.x = static_cast<const char*>(a.x) + (size_t)(m0 * a.K) * xb;
+        c.y = static_cast<char*>(a.y) + (size_t)(m0 * a.N) * yb;
+        e = HQ_CAT(launch_qmvx_t_b, HQ_BITS)(c);
+      }
+      return e;
+    }
+  }
+  if (gemm_ok) {
     if (a.w2) return a.xdt == DT_BF16 ? run_qgemm_g<DT_BF16, true>(a) : run_qgemm_g<DT_F16, true>(a);
     return a.xdt == DT_BF16 ? run_qgemm_g<DT_BF16>(a) : run_qgemm_g<DT_F16>(a);
   }

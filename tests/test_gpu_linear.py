@@ -38,8 +38,9 @@ def _round_sum(y_bits, bias_bits, dt):
 
 # (M, N, K, x dtype, scale dtype): every transpose=true kernel family --
 # streaming decode GEMV (K > 2048, M in 1, 2, 4, 8), persistent GEMV (K = 2048,
-# M = 3), batched GEMV (K % 1024 != 0), the VALU GEMV (fp32 x), the general
-# GEMM (M = 20, mixed dtypes) and the large-tile GEMM (M >= 128).
+# M = 3), batched GEMV (K % 1024 != 0), the VALU GEMV (fp32 x), 8-row GEMV
+# launches for 9-32 rows on few W rows (M = 12, 26), the general GEMM (mixed
+# dtypes), the large-tile GEMM (M = 20, M >= 128).
 CASES = [
     (1, 1024, 4096, O.BF16, O.BF16),
     (2, 4096, 4096, O.BF16, O.BF16),
@@ -49,6 +50,8 @@ CASES = [
     (1, 320, 640, O.BF16, O.BF16),
     (2, 256, 512, O.F32, O.F32),
     (20, 384, 1024, O.BF16, O.BF16),
+    (12, 1024, 4096, O.BF16, O.BF16),
+    (26, 512, 4096, O.F16, O.F16),
     (33, 256, 512, O.F16, O.BF16),
     (256, 640, 1024, O.BF16, O.BF16),
     (200, 512, 768, O.F16, O.F16),

@@ -449,6 +449,34 @@ def test_qmv_few_rows_vocabulary_dense_form(dev, M):
     assert rel_err(to_host_f64(y)[:, rows], ref) <= 1e-2
 
 
+@pytest.mark.parametrize("M,K,g", [(9, 4096, 64), (12, 2048, 128), (16, 4096, 64)])
+def test_qmm_nine_to_sixteen_rows_dense_form(dev, M, K, g):
+    """9-16 rows of 4-bit weights with a ragged N of 14,003 rows run the
+    streaming kernel's dense form in place of the GEMM's 64 x 64 tiles;
+    sampled weight rows vs the oracle."""
+    N, dt = 14003, O.BF16
+    w, s, b = quant(N + M + K, N, K, 4, g, dt)
+    x = x_of(M + K, (M, K), dt)
+    y = ops.quantized_matmul(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                             to_dev(b, dt, dev), True, g, 4)
+    rows = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(N + M).integers(0, N, 96)]))
+    ref = O.qmm_f64(x, dt, w[rows], s[rows], b[rows], dt, g, 4)
+    assert rel_err(to_host_f64(y)[:, rows], ref) <= 1e-2
+
+
+@pytest.mark.parametrize("M,N,K,bits,g", [(20, 1000, 4096, 4, 64), (31, 1000, 4096, 4, 64),
+                                         (12, 2000, 4096, 8, 128), (9, 4100, 4096, 2, 32),
+                                         (17, 6000, 4096, 3, 64)])
+def test_qmm_few_output_tiles_gemv_launches(dev, M, N, K, bits, g):
+    """9-32 rows against few W rows run as ceil(M / 8) GEMV launches (the
+    last one ragged: 4, 7, 1 and 1 rows here); sampled rows vs the oracle."""
+    _sampled_rows_check(dev, M, N, K, bits, g, seed=M + N + bits, n_rows=96)
+
+
+def test_qmm_few_output_tiles_gemv_launches_f16(dev):
+    _qmm_check(dev, 12, 300, 4096, 4, 64, O.F16, O.F16, seed=12)
+
+
 @pytest.mark.parametrize("M,N,K,bits,g", [
     (M, N, K, bits, g)
     for (M, N, K) in [(803, 14653, 1024), (285, 10990, 1024), (803, 9325, 1024),
