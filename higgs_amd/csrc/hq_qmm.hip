@@ -12,6 +12,7 @@
 // with fp32 accumulation. Gathered batches (gather_qmm with M > 8) use
 // blockIdx.z.
 #include <algorithm>
+#include <type_traits>
 
 #include "hq_common.hpp"
 #include "hq_device.hpp"
@@ -258,6 +259,15 @@ template <> struct GTile<64> {
 };
 constexpr int GLD = GBK + 16;  // LDS row stride (elements): 160 B (fewest bank conflicts measured)
 
+// Least common multiple of two ring depths and 2 (the LDS buffer count): the
+// unrolled group in which every ring slot and LDS buffer is a compile-time index.
+constexpr int ring_group(int a, int b) {
+  int x = a, y = b;
+  while (y) { const int t = x % y; x = y; y = t; }
+  const int l = a / x * b;
+  return l % 2 ? 2 * l : l;
+}
+
 struct GKern {
   void* y;
   const void* x;
@@ -384,11 +394,34 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   const ST* sg = (const ST*)(w_up ? a.s2 : a.s);
   const ST* bg = (const ST*)(w_up ? a.b2 : a.b);
 
-  // Scale and bias stay raw 16-bit in the ring and are widened where they are
-  // used: widening at the load makes the compiler wait for that load at once.
+  // Register rings, indexed by compile-time slots inside an unrolled group of
+  // kG steps: x of step kt + kRD and W of step kt + kWD are loaded at the end
+  // of step kt. x reaches LDS at the end of step kt + kRD - 1, after kRD - 1
+  // steps of MFMAs; W is dequantized into LDS from the start of step
+  // kt + kWD - 1, so it has kWD - 2 steps of cover. (Rotating registers by
+  // copies instead would make every copy wait for the loads just issued.)
+  // x depth 2 with whole groups free of branches measured fastest (M = 2048
+  // gate/up 300 -> 287 us, fused SwiGLU 561 -> 524 us, M = 256 and 512 2-6 %
+  // faster); the 128 x 128 tile without split-K keeps depth 3 and per-step
+  // tests, which hold it at two waves per SIMD (depth 2 unbranched took it
+  // to one: down 337 -> 347 us). The 64 x 128 and 96 x 128 split-K tiles
+  // give W a third slot (M = 512 4096 x 4096 38.8 -> 35.9 us, 4096 x 14336
+  // 130 -> 119, M = 127 14336 x 4096 40.6 -> 38.1, M = 512 6144 x 2048
+  // 27.3 -> 26.9); the 64 x 64 and 128 x 128 split-K tiles measured 2-5 %
+  // slower with it (their steps are bound by the dequantization VALU and
+  // the shared barrier, not by the W loads).
+  constexpr int kRD = (SZ == 128 && KS == 1) ? 3 : 2;
+  constexpr int kWD = (SZ == 192 || SZ == 96) && KS > 1 ? kRD + 1 : kRD;
+  constexpr int kG = ring_group(kRD, kWD);
+  using SV = std::conditional_t<(kWD > kRD), uint32_t, uint16_t>;
+
+  // Scale and bias stay raw 16-bit values in the ring and are widened where
+  // they are used: widening at the load makes the compiler wait for that load
+  // at once. (With the deeper W ring they sit zero-extended in 32-bit slots,
+  // so no zero-extension of its own gets placed ahead of their use.)
   struct WPre {
     uint32_t wd[BITS];
-    uint16_t sv, bv;
+    SV sv, bv;
   };
   auto wload = [&](WPre& p, int k0) {
     load_pack<BITS>(wg + woff + (uint32_t)(k0 >> 5) * BITS, p.wd);
@@ -397,11 +430,12 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
     p.bv = bg[gi];
   };
   // Quarter qq (8 elements) of this thread's pack, one 16-byte LDS store.
-  auto wchunk = [&](const WPre& p, int buf, int qq) {
+  auto wchunk = [&](const WPre& p, float sf, float bf, int buf, int qq) {
     uint16_t* dst = As + buf * GBN * GLD + wr * GLD + wp * 32 + qq * 8;
-    const u32x4 v = deq8<BITS, CT>(p.wd, qq, DT_<CT>::to_f32(p.sv), DT_<CT>::to_f32(p.bv));
+    const u32x4 v = deq8<BITS, CT>(p.wd, qq, sf, bf);
     if (w_row) *reinterpret_cast<u32x4*>(dst) = v;
   };
+
 
   floatx4 acc[NI][NJ];
 #pragma unroll
@@ -414,6 +448,17 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
   auto step = [&](int buf, const WPre& wn_) {
     const uint16_t* as = As + buf * GBN * GLD;
     const uint16_t* bs = Bs + buf * GBM * GLD;
+    // With the deeper W ring, scale and bias are widened here, where this
+    // step first uses them: the empty volatile asm keeps the compiler from
+    // widening them next to their loads (which makes it wait for those loads
+    // there, kWD - 1 steps early).
+    float sf = 0.f, bf = 0.f;
+    if constexpr (kWD > kRD) {
+      uint32_t sraw = wn_.sv, braw = wn_.bv;
+      asm volatile("" : "+v"(sraw), "+v"(braw));
+      sf = DT_<CT>::to_f32((uint16_t)sraw);
+      bf = DT_<CT>::to_f32((uint16_t)braw);
+    }
 #pragma unroll
     for (int ks = 0; ks < GBK / 32; ks++) {
       const int kofs = ks * 32 + (lane >> 4) * 8;
@@ -429,24 +474,18 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
             *reinterpret_cast<const u32x4*>(as + (wn * TL::WN + i * 16 + (lane & 15)) * GLD + kofs));
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[i][j] = T::mma(fa, fb[j], acc[i][j]);
-        if (i % ((NI + 1) / 2) == 0) wchunk(wn_, buf ^ 1, ks * 2 + i / ((NI + 1) / 2));
+        if (i % ((NI + 1) / 2) == 0) {
+          const int qq = ks * 2 + i / ((NI + 1) / 2);
+          if constexpr (kWD > kRD) wchunk(wn_, sf, bf, buf ^ 1, qq);
+          else wchunk(wn_, DT_<CT>::to_f32(wn_.sv), DT_<CT>::to_f32(wn_.bv), buf ^ 1, qq);
+        }
       }
     }
   };
 
-  // Register ring of kRD K-steps for x and W, indexed by compile-time slots
-  // inside an unrolled group of steps: the loads of step kt + kRD are issued
-  // at step kt and reach LDS at step kt + kRD - 1, so kRD - 1 steps of MFMAs
-  // cover their latency. (Rotating registers by copies instead would make
-  // every copy wait for the loads just issued.) Depth 2 with whole groups
-  // free of branches measured fastest (M = 2048 gate/up 300 -> 287 us, fused
-  // SwiGLU 561 -> 524 us, M = 256 and 512 2-6 % faster); the 128 x 128 tile
-  // without split-K keeps depth 3 and per-step tests, which hold it at two
-  // waves per SIMD (depth 2 unbranched took it to one: down 337 -> 347 us).
-  constexpr int kRD = (SZ == 128 && KS == 1) ? 3 : 2;
   const int nk = K / (GBK * KS);   // K steps of this group (the launcher checks KS | K / GBK)
   const int kb = kg * nk * GBK;    // first K element of this group's slice
-  WPre wr_[kRD];
+  WPre wr_[kWD];
   u32x4 xr_[kRD][XJ];
   auto xload_to = [&](u32x4 (&d)[XJ], int k0) {
 #pragma unroll
@@ -458,43 +497,60 @@ __global__ __launch_bounds__(GTile<SZ>::WAVES * 64 * KS) void qgemm_kernel(GKern
     for (int j = 0; j < XJ; j++)
       *reinterpret_cast<u32x4*>(bs + (xr + (NT / 8) * j) * GLD + xc * 8) = d[j];
   };
+  if constexpr (kWD > kRD) {
+    // Prologue loads in the loop's own order (x of a step, then W of the
+    // step kWD - kRD later), pinned against reordering: the loop header's
+    // waits are merged over the prologue and the loop's back edge, so a
+    // different order here would make every group's first step wait for
+    // more loads.
+    wload(wr_[0], kb);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int d = 0; d < kRD; d++) {
-    xload_to(xr_[d], kb + min(d, nk - 1) * GBK);
-    wload(wr_[d], kb + min(d, nk - 1) * GBK);
+    for (int d = 0; d < kRD || d + 1 < kWD; d++) {
+      if (d < kRD) xload_to(xr_[d], kb + min(d, nk - 1) * GBK);
+      if (d + 1 < kWD) wload(wr_[d + 1], kb + min(d + 1, nk - 1) * GBK);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+#pragma unroll
+    for (int d = 0; d < kRD; d++) {
+      xload_to(xr_[d], kb + min(d, nk - 1) * GBK);
+      wload(wr_[d], kb + min(d, nk - 1) * GBK);
+    }
   }
 #pragma unroll
-  for (int c = 0; c < 4; c++) wchunk(wr_[0], 0, c);
+  for (int c = 0; c < 4; c++)
+    wchunk(wr_[0], DT_<CT>::to_f32((uint16_t)wr_[0].sv), DT_<CT>::to_f32((uint16_t)wr_[0].bv), 0, c);
   xstore_from(xr_[0], 0);
   __syncthreads();
-  // One K step at position dd of a group (ring slot dd % kRD, LDS buffer
-  // dd & 1).
+  // One K step at position dd of a group (ring slots dd % kRD and dd % kWD,
+  // LDS buffer dd & 1).
   auto kstep = [&](int kt, int dd) {
-    const int d = dd % kRD, buf = dd & 1;
-    step(buf, wr_[(d + 1) % kRD]);
-    xstore_from(xr_[(d + 1) % kRD], buf ^ 1);
+    const int buf = dd & 1;
+    step(buf, wr_[(dd + 1) % kWD]);
+    xstore_from(xr_[(dd + 1) % kRD], buf ^ 1);
     // past the end: reload the last step (unused)
-    xload_to(xr_[d], kb + min(kt + kRD, nk - 1) * GBK);
-    wload(wr_[d], kb + min(kt + kRD, nk - 1) * GBK);
+    xload_to(xr_[dd % kRD], kb + min(kt + kRD, nk - 1) * GBK);
+    wload(wr_[dd % kWD], kb + min(kt + kWD, nk - 1) * GBK);
     __syncthreads();
   };
   if constexpr (kRD % 2 == 0) {
-    // Whole groups of kRD steps run with no branch between their steps (a
+    // Whole groups of kG steps run with no branch between their steps (a
     // load issued under a branch makes the compiler drain every load in
     // flight at the join); the steps of a last partial group are tested one
     // by one.
     int kt0 = 0;
-    for (; kt0 + kRD <= nk; kt0 += kRD) {
+    for (; kt0 + kG <= nk; kt0 += kG) {
 #pragma unroll
-      for (int dd = 0; dd < kRD; dd++) kstep(kt0 + dd, dd);
+      for (int dd = 0; dd < kG; dd++) kstep(kt0 + dd, dd);
     }
 #pragma unroll
-    for (int dd = 0; dd < kRD - 1; dd++)
+    for (int dd = 0; dd < kG - 1; dd++)
       if (kt0 + dd < nk) kstep(kt0 + dd, dd);
   } else {
-    for (int kt0 = 0; kt0 < nk; kt0 += 2 * kRD) {
+    for (int kt0 = 0; kt0 < nk; kt0 += kG) {
 #pragma unroll
-      for (int dd = 0; dd < 2 * kRD; dd++)
+      for (int dd = 0; dd < kG; dd++)
         if (kt0 + dd < nk) kstep(kt0 + dd, dd);
     }
   }
