@@ -65,6 +65,7 @@ hipError_t dispatch_q(int bits, const hq::QArgs& a, int which) {
     if (which == 1) return hq::launch_qmm_t_b##B(a);   \
     if (which == 3) return hq::launch_qmvx_t_b##B(a);  \
     if (which == 4) return hq::launch_gqmm_t_b##B(a);  \
+    if (which == 5) return hq::launch_gqms_dense_t_b##B(a); \
     return hq::launch_qmv_n_b##B(a);
   switch (bits) {
     HQ_Q_CASE(2)
@@ -322,7 +323,21 @@ int hq_quantized_matmul_swiglu(void* h, const void* x, const uint32_t* w_gate,
   a.group_size = group_size; a.xdt = x_dtype; a.sdt = s_dtype; a.sorted = 0;
   a.stream = (hipStream_t)stream;
   hipError_t e = hipSuccess;
-  if (gemm) {
+  bool dense = false;
+  if (!gemm && M > hq::kQmvMaxM) {
+    // 9-11 rows: the streaming kernel's dense form where it takes the shape
+    // (4-bit, N >= 8192, K 2048 or 4096; the GEMM tries it first from 12
+    // rows, the GEMV launcher at 8)
+    a.M = M;
+    e = dispatch_q(bits, a, 5);
+    dense = e != hipErrorNotSupported;
+    if (!dense) {
+      (void)hipGetLastError();
+      e = hipSuccess;
+    }
+  }
+  if (dense) {
+  } else if (gemm) {
     a.M = M;
     e = dispatch_q(bits, a, 1);
   } else {

@@ -102,8 +102,9 @@ constexpr int kMR = 64;  // x rows per block pass (four 16-row MFMA tiles)
 // Row stride (floats) of the group sums in LDS for GQ groups per lane group:
 // the fp32 MFMA's A read of lane group q starts q * GQ rows down, and a stride
 // with GQ * stride = 16 (mod 64) puts the four lane groups on disjoint banks.
-constexpr int xsum_stride(int gq) {
-  int s = kMR;
+// At least `rows` floats per row (the rows a block pass stages).
+constexpr int xsum_stride(int gq, int rows) {
+  int s = rows;
   while ((gq * s) % 64 != 16) s++;
   return s;
 }
@@ -142,12 +143,15 @@ template <int KC, bool SWI, bool DENSE = false> struct GSShape {
   static constexpr int WPT = DENSE ? 2 : 1;   // waves per tile
   static constexpr int TPW = 8 / WPT;         // tiles in flight per block
   static constexpr int RED = DENSE ? 8 * 64 * 16 * NS : 0;  // LDS for the cross-wave sums
+  // group-sum rows: the dense SwiGLU form strides them for its 16 rows (at
+  // K = 4096 its LDS would not fit otherwise); every other form for 64
+  static constexpr int XSR = SWI && DENSE ? MR : kMR;
 };
 // LDS of one block: group sums, the out-of-range flags, the x rows.
 template <int GS, int KC, bool SWI, bool DENSE = false>
 constexpr int gx_lds_bytes() {
   using SH = GSShape<KC, SWI, DENSE>;
-  return (KC * 256 / GS) * xsum_stride(SH::CP * (256 / GS) / 4) * 4 + SH::MR * 4 +
+  return (KC * 256 / GS) * xsum_stride(SH::CP * (256 / GS) / 4, SH::XSR) * 4 + SH::MR * 4 +
          SH::MR * xrow_elems(KC * 256) * 2 + SH::RED;
 }
 
@@ -167,7 +171,7 @@ __global__ __launch_bounds__(512, 2) void gqms_kernel(GSKern a) {
   constexpr int NWL = NS * CP * 2;  // weight load instructions per item (16 bytes per lane)
   static_assert(WPG == 2 || WPG == 4, "group size 64 or 128");
   static_assert(KC % CP == 0 && GPP % 4 == 0, "whole parts, whole fp32-MFMA steps of groups");
-  constexpr int XSS = xsum_stride(GQ);
+  constexpr int XSS = xsum_stride(GQ, SH::XSR);
   static_assert(gx_lds_bytes<GS, KC, SWI, DENSE>() <= 160 * 1024, "x rows fit the LDS");
   static_assert(KP % WPT == 0, "whole parts per wave");
   using T = SMma<XDT>;
@@ -625,14 +629,19 @@ hipError_t run_gqms_g(const QArgs& a) {
   return a.group_size == 64 ? run_gqms_k<XDT, 64, SWI>(a) : run_gqms_k<XDT, 128, SWI>(a);
 }
 
-template <int XDT, int GS>
+template <int XDT, int GS, bool SWI>
 hipError_t run_gqms_dense_k(const QArgs& a) {
   switch (a.K / 256) {
-    case 8: return run_gqms<XDT, GS, 8, false, true>(a);
-    case 16: return run_gqms<XDT, GS, 16, false, true>(a);
+    case 8: return run_gqms<XDT, GS, 8, SWI, true>(a);
+    case 16: return run_gqms<XDT, GS, 16, SWI, true>(a);
     default: break;
   }
   return hipErrorNotSupported;
+}
+
+template <int XDT, int GS>
+hipError_t run_gqms_dense_s(const QArgs& a) {
+  return a.w2 ? run_gqms_dense_k<XDT, GS, true>(a) : run_gqms_dense_k<XDT, GS, false>(a);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -679,7 +688,7 @@ hipError_t HQ_CAT(launch_gqms_dense_t_b, HQ_BITS)(const QArgs& a) {
     (void)a;
     return hipErrorNotSupported;
   } else {
-    if (a.w2 || a.lb || a.lhs || a.rhs || a.batch != 1 || a.xdt != a.sdt || a.xdt == DT_F32)
+    if (a.lb || a.lhs || a.rhs || a.batch != 1 || a.xdt != a.sdt || a.xdt == DT_F32)
       return hipErrorNotSupported;
     // 4-7 rows only at vocabulary-sized N (its cost hardly depends on the
     // row count: below 8 rows the GEMV kernels win on smaller N)
@@ -687,12 +696,13 @@ hipError_t HQ_CAT(launch_gqms_dense_t_b, HQ_BITS)(const QArgs& a) {
       return hipErrorNotSupported;
     if (a.group_size != 64 && a.group_size != 128) return hipErrorNotSupported;
     if (!aligned16(a.s) || !aligned16(a.b)) return hipErrorNotSupported;
+    if (a.w2 && (!aligned16(a.s2) || !aligned16(a.b2))) return hipErrorNotSupported;
     QArgs d = a;
     d.x_batch = 1;
     d.x_rep = 1;
     d.w_batch = 1;
-    return a.xdt == DT_BF16 ? (a.group_size == 64 ? run_gqms_dense_k<DT_BF16, 64>(d) : run_gqms_dense_k<DT_BF16, 128>(d))
-                            : (a.group_size == 64 ? run_gqms_dense_k<DT_F16, 64>(d) : run_gqms_dense_k<DT_F16, 128>(d));
+    return a.xdt == DT_BF16 ? (a.group_size == 64 ? run_gqms_dense_s<DT_BF16, 64>(d) : run_gqms_dense_s<DT_BF16, 128>(d))
+                            : (a.group_size == 64 ? run_gqms_dense_s<DT_F16, 64>(d) : run_gqms_dense_s<DT_F16, 128>(d));
   }
 }
 

@@ -1033,9 +1033,10 @@ hipError_t HQ_CAT(launch_qmm_t_b, HQ_BITS)(const QArgs& a) {
   // (the large-tile GEMM addresses x and W with 32-bit element offsets)
   const bool off32 = a.M * a.K < ((int64_t)1 << 31) &&
                      a.N * (a.K / 32) * HQ_BITS < ((int64_t)1 << 31);
-  // 9-16 rows of 4-bit weights with many output tiles: the streaming
-  // kernel's dense form (hq_gqms.hip, its own conditions)
-  if (a.M <= 16 && !a.w2) {
+  // 9-16 rows of 4-bit weights with many output tiles, plain or with the
+  // fused SwiGLU: the streaming kernel's dense form (hq_gqms.hip, its own
+  // conditions)
+  if (a.M <= 16) {
     const hipError_t ed = HQ_CAT(launch_gqms_dense_t_b, HQ_BITS)(a);
     if (ed != hipErrorNotSupported) return ed;
   }

@@ -108,6 +108,21 @@ def test_fused_swiglu_gemm_tile_forms(dev, M):
     assert rel_err(to_host_f64(h)[:, cols], ref) <= 1e-2
 
 
+@pytest.mark.parametrize("M", [8, 9, 12, 16])
+@pytest.mark.parametrize("K,g", [(4096, 64), (2048, 128)])
+def test_fused_swiglu_dense_streaming_form(dev, M, K, g):
+    """8-16 rows against 14,003 gate/up columns (ragged) of 4-bit weights:
+    the streaming kernel's dense form with both projections per tile (group
+    sums strided for its 16 rows); 96 sampled output columns vs the oracle."""
+    N, dt, bits = 14003, O.BF16, 4
+    x, w, s, b = _dense_case(1700 + M + K, M, N, K, bits, g, dt)
+    h = ops.dense_hidden_fused(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                               to_dev(b, dt, dev), N, g, bits)
+    cols = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(M + K).integers(0, N, 96)]))
+    ref = _swiglu_ref(x, dt, w[cols], s[cols], b[cols], w[N + cols], s[N + cols], b[N + cols], g, bits)
+    assert rel_err(to_host_f64(h)[:, cols], ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 256])
 def test_fused_equals_separate(dev, M):
     # qwen3_next.rs:13132-13169: fused gate||up == separate projections
