@@ -37,7 +37,8 @@ Printed JSON line (one, on stdout):
   decode_fused  the same decode step with the launches fused: q|k|v
                 concatenated (one launch), gate/up + SwiGLU in one launch
                 (hq_quantized_matmul_swiglu, the reference's
-                dense_hidden_fused), o, down, lm_head: 129 launches
+                dense_hidden_fused), o, down, lm_head: 129 launches;
+                at --batch rows and at B = 1, 4, 8 ("batches")
   cpu_baseline  the CPU oracle's MLX-style quantized_matmul on every host
                 CPU the job may run on (and on 1 thread), on a bounded sample
                 of the same workload (layer 0's seven projections at B), with
@@ -283,7 +284,8 @@ def bench_prefill_chunks(dev, steps):
 class FusedPlan:
     """The decode step with fused launches: per layer q|k|v concatenated
     along N, o, gate/up with the SwiGLU epilogue, down; then lm_head.
-    Weights are concatenated copies of the Model's (same bytes)."""
+    Weights are concatenated copies of the Model's (same bytes). Buffers
+    hold B rows; use(b) sets the calls and bytes of a step of b <= B rows."""
 
     def __init__(self, model, B, dev):
         import torch
@@ -299,7 +301,6 @@ class FusedPlan:
         self.yl = torch.empty((B, VOCAB), dtype=torch.bfloat16, device=dev)
         self.keep = []
         self.plan = []
-        self.bytes = 0
         for ws in model.layers:
             qkv = [torch.cat([ws[n][i] for n in ("q", "k", "v")]) for i in range(3)]
             gu = [torch.cat([ws[n][i] for n in ("gate", "up")]) for i in range(3)]
@@ -308,11 +309,17 @@ class FusedPlan:
             self.plan.append(("mm", self.yo, self.x, ws["o"], HIDDEN, HIDDEN))
             self.plan.append(("swiglu", self.yh, self.x, gu, INTER, HIDDEN))
             self.plan.append(("mm", self.yo, self.h, ws["down"], HIDDEN, INTER))
-            self.bytes += (qmv_bytes(B, 6144, HIDDEN) + qmv_bytes(B, HIDDEN, HIDDEN) +
-                           qmv_bytes(B, 2 * INTER, HIDDEN) - 2 * B * INTER +
-                           qmv_bytes(B, HIDDEN, INTER))
         self.plan.append(("mm", self.yl, self.x, model.lm_head, VOCAB, HIDDEN))
-        self.bytes += qmv_bytes(B, VOCAB, HIDDEN)
+        self.Bmax = B
+        self.use(B)
+        torch.cuda.synchronize()
+
+    def use(self, B):
+        assert 1 <= B <= self.Bmax
+        layers = (len(self.plan) - 1) // 4
+        self.bytes = layers * (qmv_bytes(B, 6144, HIDDEN) + qmv_bytes(B, HIDDEN, HIDDEN) +
+                               qmv_bytes(B, 2 * INTER, HIDDEN) - 2 * B * INTER +
+                               qmv_bytes(B, HIDDEN, INTER)) + qmv_bytes(B, VOCAB, HIDDEN)
         self.B = B
         rows = lambda t, n: t.data_ptr() + n * t.stride(0) * t.element_size()
         self.calls = []
@@ -324,7 +331,6 @@ class FusedPlan:
                 self.calls.append((1, (y.data_ptr(), x.data_ptr(), w.data_ptr(), s.data_ptr(),
                                        b.data_ptr(), rows(w, N), rows(s, N), rows(b, N), B, N, K,
                                        GROUP, BITS, 2, 2)))
-        torch.cuda.synchronize()
 
     def run(self, stream_ptr):
         fm, fs = self.lib.hq_quantized_matmul, self.lib.hq_quantized_matmul_swiglu
@@ -641,12 +647,16 @@ def bench_mid_rows(model, dev, steps):
 def bench_fused(model, args, dev):
     import torch
 
-    fp = FusedPlan(model, args.batch, dev)
-    mf = time_graph(fp.run, args.steps, 2, dev)
-    r = {"batch": args.batch, "launches": len(fp.calls), "ms_per_step": round(mf, 4),
-         "GB/s": round(fp.bytes / (mf * 1e-3) / 1e9, 1),
-         "frac": round(fp.bytes / (mf * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-         "tokens_per_s": round(1e3 / mf, 1)}
+    fp = FusedPlan(model, max(8, args.batch), dev)
+    res = {}
+    for B in sorted({args.batch, 1, 4, 8}):
+        fp.use(B)
+        mf = time_graph(fp.run, args.steps if B == args.batch else max(5, args.steps // 2), 2, dev)
+        res[B] = {"ms_per_step": round(mf, 4), "GB/s": round(fp.bytes / (mf * 1e-3) / 1e9, 1),
+                  "frac": round(fp.bytes / (mf * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                  "tokens_per_s": round(B * 1e3 / mf, 1)}
+    r = {"batch": args.batch, "launches": len(fp.calls), **res[args.batch],
+         "batches": {str(B): v for B, v in res.items() if B != args.batch}}
     del fp
     torch.cuda.empty_cache()
     return r
