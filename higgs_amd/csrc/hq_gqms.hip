@@ -676,9 +676,10 @@ hipError_t HQ_CAT(launch_gqms_t_b, HQ_BITS)(const QArgs& a) {
 }
 
 // Batched decode through the same kernel (DENSE): one product of 8-16 rows,
-// or hipErrorNotSupported: other bit widths and groups, mixed or fp32
-// dtypes, K other than 2048 or 4096, N below 8192 (fewer than 512 blocks of
-// 4 tiles), the fused SwiGLU, a linear bias, unaligned scales or biases.
+// plain or with the fused SwiGLU (both projections per tile), or
+// hipErrorNotSupported: other bit widths and groups, mixed or fp32 dtypes,
+// K other than 2048 or 4096, N below 8192 (fewer than 512 blocks of 4
+// tiles), a linear bias, unaligned scales or biases.
 // Measured against the GEMV kernels on the same data (8 rows): 14336 x 4096
 // 15.0-15.5 vs 16.6-16.7 us, 14336 x 2048 11.5 vs 15.0, 128256 x 4096 105 vs
 // 105; at 4 rows it was slower (15.3 vs 12.2 us), as its cost hardly depends

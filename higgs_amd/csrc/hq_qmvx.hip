@@ -1287,8 +1287,8 @@ hipError_t run_qmvx_m(const QArgs& a) {
 #define HQ_CAT(a, b) HQ_CAT_(a, b)
 
 hipError_t HQ_CAT(launch_qmvx_t_b, HQ_BITS)(const QArgs& a) {
-  // 8 rows of 4-bit weights with many output tiles: the streaming kernel's
-  // batched form (hq_gqms.hip)
+  // 8 rows of 4-bit weights with many output tiles, plain or with the fused
+  // SwiGLU: the streaming kernel's dense form (hq_gqms.hip)
   const hipError_t ed = HQ_CAT(launch_gqms_dense_t_b, HQ_BITS)(a);
   if (ed != hipErrorNotSupported) return ed;
   if (a.w2) {
