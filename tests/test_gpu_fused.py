@@ -123,6 +123,19 @@ def test_fused_swiglu_dense_streaming_form(dev, M, K, g):
     assert rel_err(to_host_f64(h)[:, cols], ref) <= 1e-2
 
 
+@pytest.mark.parametrize("M", [8, 13])
+def test_fused_swiglu_dense_streaming_form_f16(dev, M):
+    """The same dense form with fp16 x and scales (K = 2048, group 64)."""
+    N, K, dt, bits, g = 9000, 2048, O.F16, 4, 64
+    x, w, s, b = _dense_case(1800 + M, M, N, K, bits, g, dt)
+    h = ops.dense_hidden_fused(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                               to_dev(b, dt, dev), N, g, bits)
+    assert h.dtype == torch.float16
+    cols = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(M).integers(0, N, 96)]))
+    ref = _swiglu_ref(x, dt, w[cols], s[cols], b[cols], w[N + cols], s[N + cols], b[N + cols], g, bits)
+    assert rel_err(to_host_f64(h)[:, cols], ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 256])
 def test_fused_equals_separate(dev, M):
     # qwen3_next.rs:13132-13169: fused gate||up == separate projections

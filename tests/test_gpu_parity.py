@@ -464,6 +464,20 @@ def test_qmm_nine_to_sixteen_rows_dense_form(dev, M, K, g):
     assert rel_err(to_host_f64(y)[:, rows], ref) <= 1e-2
 
 
+def test_qmm_nine_to_sixteen_rows_dense_form_f16(dev):
+    """14 rows, fp16 x and scales, 8,200 W rows (the smallest N the dense
+    form takes, ragged), K = 4096 group 128; sampled rows vs the oracle."""
+    M, N, K, g, dt = 14, 8200, 4096, 128, O.F16
+    w, s, b = quant(M + N, N, K, 4, g, dt)
+    x = x_of(M + 3, (M, K), dt)
+    y = ops.quantized_matmul(to_dev(x, dt, dev), words_dev(w, dev), to_dev(s, dt, dev),
+                             to_dev(b, dt, dev), True, g, 4)
+    assert y.dtype == torch.float16
+    rows = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(N).integers(0, N, 96)]))
+    ref = O.qmm_f64(x, dt, w[rows], s[rows], b[rows], dt, g, 4)
+    assert rel_err(to_host_f64(y)[:, rows], ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M,N,K,bits,g", [(20, 1000, 4096, 4, 64), (31, 1000, 4096, 4, 64),
                                          (12, 2000, 4096, 8, 128), (9, 4100, 4096, 2, 32),
                                          (17, 6000, 4096, 3, 64)])
