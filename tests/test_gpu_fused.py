@@ -136,6 +136,31 @@ def test_fused_swiglu_dense_streaming_form_f16(dev, M):
     assert rel_err(to_host_f64(h)[:, cols], ref) <= 1e-2
 
 
+def _host_rows(W, S, B, cols, dev):
+    ct = torch.from_numpy(cols).to(dev)
+    return (W[ct].cpu().numpy().view(np.uint32), S[ct].cpu().view(torch.int16).numpy().view(np.uint16),
+            B[ct].cpu().view(torch.int16).numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("M", [4, 7])
+def test_fused_swiglu_dense_form_vocabulary_n(dev, M):
+    """4-7 rows against 65,600 gate/up columns (K = 2048) take the dense form
+    with both projections per tile; weights made on the device, 96 sampled
+    output columns vs the oracle."""
+    N, K, g, bits = 65600, 2048, 64, 4
+    G = gen.torch_quantized(2000 + M, N, K, bits, g, dev)
+    U = gen.torch_quantized(3000 + M, N, K, bits, g, dev)
+    X = gen.torch_x(4000 + M, (M, K), dev)
+    h = ops.swiglu_pair(X, G, U, g, bits)
+    torch.cuda.synchronize()
+    cols = np.unique(np.concatenate([[0, N - 1], np.random.default_rng(M).integers(0, N, 96)]))
+    x = X.cpu().view(torch.int16).numpy().view(np.uint16)
+    wg, sg, bg = _host_rows(*G, cols, dev)
+    wu, su, bu = _host_rows(*U, cols, dev)
+    ref = _swiglu_ref(x, O.BF16, wg, sg, bg, wu, su, bu, g, bits)
+    assert rel_err(to_host_f64(h)[:, cols], ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M", [1, 2, 4, 256])
 def test_fused_equals_separate(dev, M):
     # qwen3_next.rs:13132-13169: fused gate||up == separate projections
